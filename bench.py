@@ -1,0 +1,329 @@
+"""Benchmark of the reversible-training hot path on one MI355X.
+
+Headline (``value``): fused RMSNorm + SwiGLU forward+backward throughput in
+algorithmic HBM GB/s.  One step = RMSNorm fwd + bwd over configs[0]
+(x fp32 [14848, 256]) followed by SwiGLU fwd + bwd over configs[1]
+(gate/up fp16 [14848, 1024]), launched through the C ABI on torch's current
+stream.  Algorithmic bytes per step (each tensor read or written once):
+
+    RMSNorm fwd  x r, w r, y w, rstd w             30,469,120 B
+    RMSNorm bwd  x r, dy r, rstd r, w r, dx w, dw w 45,674,496 B
+    SwiGLU fwd   gate r, up r, out w               91,226,112 B
+    SwiGLU bwd   gate r, up r, dy r, dgate w, dup w 152,043,520 B
+    step total                                    319,413,248 B
+
+Inputs are already resident in HBM when the timed region starts.  The
+256 MB Infinity Cache would hold one step's working set, so the step rotates
+through NSETS distinct buffer sets (> 1 GB in total) and every launch reads
+data last touched a full rotation earlier.
+
+Also reported, on the same line:
+  roofline      the dominant kernel (SwiGLU backward): its algorithmic bytes
+                divided by its average duration from HIP events recorded
+                around each of its launches in the timed region, against the
+                8 TB/s HBM peak; ``traffic`` is the HBM bytes per launch
+                measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), if
+                recorded.
+  kernels       the same event timing for every kernel of the step.
+  train_step    configs[3]: midpoint-reversible 7-layer decoder step
+                (B=33, T=512, fp16 autocast, GradScaler, clip 1.0, AdamW)
+                through install_v3(split core, 8192-token MLP tiles, fused
+                SwiGLU + RMSNorm), in tokens/s.
+  cpu_baseline  the CPU oracle (oracle/kernels_ref.c, OpenMP) on the host's
+                cores: the same RMSNorm + SwiGLU step, in GB/s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "RMSNorm+SwiGLU fwd/bwd HBM GB/s (% of peak); reversible train step tokens/s"
+HBM_PEAK_GBS = 8000.0
+ROWS, D_MODEL, D_FF = 14848, 256, 1024
+RMS_FWD_BYTES = ROWS * D_MODEL * 4 * 2 + D_MODEL * 4 + ROWS * 4
+RMS_BWD_BYTES = ROWS * D_MODEL * 4 * 3 + ROWS * 4 + D_MODEL * 4 * 2
+SW_FWD_BYTES = ROWS * D_FF * 2 * 3
+SW_BWD_BYTES = ROWS * D_FF * 2 * 5
+STEP_BYTES = RMS_FWD_BYTES + RMS_BWD_BYTES + SW_FWD_BYTES + SW_BWD_BYTES
+assert STEP_BYTES == 319_413_248
+NSETS = 6  # 6 x ~243 MB > 1 GB of distinct buffers
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--train-steps", type=int, default=10)
+    p.add_argument("--train-warmup", type=int, default=3)
+    p.add_argument("--no-train-step", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bounded CPU-baseline sample length (0 disables)")
+    p.add_argument("--kernels-only", action="store_true",
+                   help="only the kernel loop (used under rocprofv3)")
+    return p.parse_args()
+
+
+class KernelStep:
+    """Preallocated buffers and direct C-ABI launches for one bench step."""
+
+    def __init__(self, dev, nsets: int):
+        import torch
+        from reversability_amd import _hip
+        self.torch = torch
+        self.lib = _hip.library()
+        eps = float(torch.finfo(torch.float32).eps)
+        g = torch.Generator().manual_seed(1337)
+        x = torch.randn(ROWS, D_MODEL, generator=g)
+        w = 1 + 0.02 * torch.randn(D_MODEL, generator=g)
+        gy = torch.randn(ROWS, D_MODEL, generator=g)
+        gate = torch.randn(ROWS, D_FF, generator=g).half()
+        up = torch.randn(ROWS, D_FF, generator=g).half()
+        sdy = torch.randn(ROWS, D_FF, generator=g).half()
+        u = torch.cat([gate, up], 1)  # packed [gate | up], the reference layout
+        ws_bytes = _hip.rmsnorm_workspace_bytes(ROWS, D_MODEL)
+        self.sets = []
+        for _ in range(nsets):
+            s = {
+                "x": x.to(dev), "w": w.to(dev), "gy": gy.to(dev),
+                "y": torch.empty(ROWS, D_MODEL, device=dev),
+                "rstd": torch.empty(ROWS, device=dev),
+                "dx": torch.empty(ROWS, D_MODEL, device=dev),
+                "dw": torch.empty(D_MODEL, device=dev),
+                "ws": torch.empty(ws_bytes // 4, device=dev),
+                "u": u.to(dev), "sdy": sdy.to(dev),
+                "o": torch.empty(ROWS, D_FF, device=dev, dtype=torch.float16),
+                "du": torch.empty(ROWS, 2 * D_FF, device=dev, dtype=torch.float16),
+            }
+            p = {k: v.data_ptr() for k, v in s.items()}
+            s["args"] = {
+                "rms_fwd": (p["x"], p["w"], p["y"], p["rstd"], ROWS, D_MODEL, eps),
+                "rms_bwd": (p["x"], p["w"], p["gy"], p["rstd"], p["dx"], p["dw"], p["ws"],
+                            ws_bytes, ROWS, D_MODEL),
+                "sw_fwd": (p["u"], 2 * D_FF, p["o"], ROWS, D_FF, _hip.RV_F16),
+                "sw_bwd": (p["u"], 2 * D_FF, p["sdy"], p["du"], ROWS, D_FF, _hip.RV_F16),
+            }
+            self.sets.append(s)
+        self.fns = {"rms_fwd": self.lib.rv_rmsnorm_fwd, "rms_bwd": self.lib.rv_rmsnorm_bwd,
+                    "sw_fwd": self.lib.rv_swiglu_fwd, "sw_bwd": self.lib.rv_swiglu_bwd}
+        self.order = ["rms_fwd", "rms_bwd", "sw_fwd", "sw_bwd"]
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run(self, i: int, events=None) -> None:
+        args = self.sets[i % len(self.sets)]["args"]
+        for name in self.order:
+            if events is not None:
+                start, stop = events[name].pop()
+                start.record()
+            rc = self.fns[name](*args[name], self.stream)
+            if events is not None:
+                stop.record()
+            if rc:
+                raise RuntimeError(f"{name} failed with status {rc}")
+
+
+def time_kernels(dev, steps: int, warmup: int):
+    import torch
+    step = KernelStep(dev, NSETS)
+    for i in range(warmup):
+        step.run(i)
+    torch.cuda.synchronize()
+    # Timed region 1: whole steps back to back (the headline).
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step.run(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # Timed region 2: the same steps with HIP events around every launch.
+    events = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(steps)] for n in step.order}
+    recorded = {n: list(v) for n, v in events.items()}
+    torch.cuda.synchronize()
+    for i in range(steps):
+        step.run(i, events)
+    torch.cuda.synchronize()
+    per_kernel = {n: sum(a.elapsed_time(b) for a, b in recorded[n]) / steps for n in step.order}
+    # spot-check the outputs of the last set against a second launch (determinism)
+    s = step.sets[(steps - 1) % NSETS]
+    ref_dx, ref_du = s["dx"].clone(), s["du"].clone()
+    step.run(steps - 1)
+    torch.cuda.synchronize()
+    if not (torch.equal(ref_dx, s["dx"]) and torch.equal(ref_du, s["du"])):
+        raise RuntimeError("kernel outputs are not run-to-run deterministic")
+    return wall / steps, per_kernel
+
+
+def kernel_loop_only(dev, steps: int, warmup: int) -> None:
+    """The kernel loop alone (rocprofv3 --kernel-trace / --pmc target)."""
+    import torch
+    step = KernelStep(dev, NSETS)
+    for i in range(warmup + steps):
+        step.run(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"kernels_only": True, "steps": steps, "warmup": warmup}), flush=True)
+
+
+def train_step_bench(dev, steps: int, warmup: int):
+    """midpoint-reversible 7-layer step, B=33, T=512, tokens/s."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    from reversability_amd import build_model
+    from reversability_amd.optimized_v3 import install_v3
+
+    batch, length = 33, 512
+    config = {"model": {"vocab_size": 50257, "max_sequence_length": 512, "n_layers": 7,
+                        "n_heads": 8, "d_model": 256, "d_ff": 1024},
+              "method": "midpoint", "step_size": 0.5}
+    torch.manual_seed(1337)
+    model = build_model(config).to(dev)
+    install_v3(model, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    scaler = torch.amp.GradScaler("cuda")
+    # one uint16 stream of B*T+1 uniform ids; x = stream[:-1], y = stream[1:]
+    stream = np.random.default_rng(1337).integers(0, 50257, batch * length + 1).astype(np.uint16)
+    x = torch.from_numpy(stream[:-1].astype(np.int64).reshape(batch, length)).to(dev)
+    y = torch.from_numpy(stream[1:].astype(np.int64).reshape(batch, length)).to(dev)
+    targets = batch * length
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            logits = model(x)
+            loss = F.cross_entropy(logits.flatten(0, 1), y.flatten(), reduction="sum")
+            scaler.scale(loss / targets).backward()
+        scaler.unscale_(opt)
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        scaler.step(opt)
+        scaler.update()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"tokens_per_s": targets / dt, "ms_per_step": dt * 1e3,
+            "loss": float(loss.item()) / targets, "steps": steps, "warmup": warmup,
+            "config": {"workload": "configs[3] midpoint 7L d256 h8 ff1024 vocab50257",
+                       "global_batch": batch, "seq_len": length,
+                       "core_mode": "split", "mlp_tokens": 8192, "precision": "fp16-autocast"},
+            "data": "synthetic uniform token ids (seed 1337)"}
+
+
+def cpu_baseline(seconds: float):
+    """Oracle (C, OpenMP) on this host's cores: the same RMSNorm+SwiGLU step."""
+    import numpy as np
+    import oracle
+    threads = len(os.sched_getaffinity(0))
+    oracle.set_num_threads(threads)
+    r = np.random.default_rng(1337)
+    x = r.standard_normal((ROWS, D_MODEL)).astype(np.float32)
+    w = (1 + 0.02 * r.standard_normal(D_MODEL)).astype(np.float32)
+    gy = r.standard_normal((ROWS, D_MODEL)).astype(np.float32)
+    u = r.standard_normal((ROWS, 2 * D_FF)).astype(np.float16)
+    sdy = r.standard_normal((ROWS, D_FF)).astype(np.float16)
+    eps = float(np.finfo(np.float32).eps)
+
+    def one():
+        oracle.rmsnorm_fwd(x, w, eps)
+        oracle.rmsnorm_bwd(x, w, gy, eps)
+        oracle.swiglu_fwd(u)
+        oracle.swiglu_bwd(u, sdy)
+
+    one()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    per = dt / n
+    return {"value": STEP_BYTES / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": per * 1e3,
+            "sample": f"{n} full steps (RMSNorm [14848,256] fwd+bwd + SwiGLU [14848,1024] "
+                      f"fwd+bwd) of oracle/kernels_ref.c with OpenMP, {dt:.1f} s"}
+
+
+def load_traffic():
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get("swiglu_bwd_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(collectives, sharding and rank code are out of scope); run with --gpus 1.",
+              file=sys.stderr, flush=True)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    if args.kernels_only:
+        kernel_loop_only(dev, args.steps, args.warmup)
+        return 0
+    ms_step_s, per_kernel = time_kernels(dev, args.steps, args.warmup)
+    value = STEP_BYTES / ms_step_s / 1e9
+    bytes_by = {"rms_fwd": RMS_FWD_BYTES, "rms_bwd": RMS_BWD_BYTES,
+                "sw_fwd": SW_FWD_BYTES, "sw_bwd": SW_BWD_BYTES}
+    kernels = {n: {"avg_us": per_kernel[n] * 1e3, "algorithmic_bytes": bytes_by[n],
+                   "GBps": bytes_by[n] / (per_kernel[n] * 1e-3) / 1e9,
+                   "frac_of_peak": bytes_by[n] / (per_kernel[n] * 1e-3) / 1e9 / HBM_PEAK_GBS}
+               for n in per_kernel}
+    achieved = kernels["sw_bwd"]["GBps"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 (RMSNorm) + fp16 I/O, fp32 math (SwiGLU)",
+        "data": "synthetic, seed 1337 (x, dy ~N(0,1); w = 1 + N(0, 0.02))",
+        "config": {"workload": "configs[0] RMSNorm fwd+bwd [14848,256] fp32 + "
+                               "configs[1] SwiGLU fwd+bwd [14848,1024] fp16",
+                   "buffer_sets": NSETS, "step_bytes": STEP_BYTES},
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "kernel": "swiglu_bwd_vec<fp16>",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+                     "algorithmic_bytes": SW_BWD_BYTES},
+        "kernels": kernels,
+    }
+    if not args.no_train_step:
+        line["train_step"] = train_step_bench(dev, args.train_steps, args.train_warmup)
+    if args.cpu_seconds > 0:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,164 @@
+/*
+ * reversibility_hip.h -- C ABI of the MI355X (gfx950) kernels behind the
+ * reversible-training hot path: fused RMSNorm, fused SwiGLU and the fused
+ * reversible residual updates (midpoint and Hamiltonian-Euler).
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers (HIP global memory).  Tensors are dense and
+ *     row-major; a row is `width` (or `ld`) elements long.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default
+ *     stream).  Every call is asynchronous: it enqueues kernels on `stream`,
+ *     never synchronises the host and never allocates memory.
+ *   - The return value is an rv_status: 0 on success; otherwise the launch did
+ *     not happen (argument errors) or HIP reported an error at launch time.
+ *     rv_status_string() names a code.
+ *   - Results do not depend on the launch shape or on the number of compute
+ *     units: every reduction has a fixed order, there are no float atomics, and
+ *     two calls on identical inputs give bit-identical outputs.
+ *   - Floating-point expressions keep the operation order of the reference's
+ *     kernels and are compiled without FMA contraction.
+ *
+ * Reference interfaces each entry point replaces are cited as
+ * path:line under the LokeshJatangi/Reversability source tree.
+ */
+#ifndef REVERSIBILITY_HIP_H
+#define REVERSIBILITY_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum rv_status {
+  RV_OK = 0,
+  RV_ERR_NULL_POINTER = 1,   /* a required pointer is NULL                     */
+  RV_ERR_BAD_SIZE = 2,       /* negative/zero size, ld < width, ...            */
+  RV_ERR_UNSUPPORTED = 3,    /* dtype or width outside what the kernels cover  */
+  RV_ERR_WORKSPACE = 4,      /* workspace missing or smaller than required     */
+  RV_ERR_HIP = 5             /* HIP runtime reported an error at launch        */
+} rv_status;
+
+typedef enum rv_dtype {
+  RV_F32 = 0,
+  RV_F16 = 1,
+  RV_BF16 = 2,
+  RV_F64 = 3
+} rv_dtype;
+
+/* Human-readable name of a status code (static storage). */
+const char* rv_status_string(int status);
+
+/* Last HIP error text seen by this thread's most recent failing call. */
+const char* rv_last_error(void);
+
+/* ABI version of this header: bumped when a signature changes. */
+int rv_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm over the last dimension, FP32.
+ *   y[r, c]  = (x[r, c] * rstd[r]) * w[c]
+ *   rstd[r]  = rsqrt(sum_c x[r, c]^2 / width + eps)
+ * Replaces _rms_forward + FusedRMSNorm.forward
+ *   (src/reversibility/kernels_v3.py:9-16, 51-62).
+ * width <= 4096.
+ */
+int rv_rmsnorm_fwd(const float* x, const float* w, float* y, float* rstd,
+                   int64_t rows, int64_t width, float eps, void* stream);
+
+/* Bytes of scratch rv_rmsnorm_bwd needs for (rows, width) on the current
+ * device.  Returns a negative rv_status on bad sizes. */
+int64_t rv_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t width);
+
+/* RMSNorm backward, FP32, single pass over x and dy:
+ *   g        = dy * w
+ *   dx[r, :] = (g - x * ((sum_c g*x) / width * rstd * rstd)) * rstd
+ *   dw[c]    = sum_r dy[r, c] * (x[r, c] * rstd[r])
+ * dw is reduced from per-block partial sums in a fixed order (second, small
+ * kernel).  `workspace` is device memory of at least
+ * rv_rmsnorm_bwd_workspace_bytes(rows, width) bytes; its contents on entry
+ * do not matter.
+ * Replaces _rms_dx + _rms_dw_partials + _rms_dw_reduce + FusedRMSNorm.backward
+ *   (src/reversibility/kernels_v3.py:19-48, 64-74).
+ */
+int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
+                   const float* rstd, float* dx, float* dw, void* workspace,
+                   int64_t workspace_bytes, int64_t rows, int64_t width,
+                   void* stream);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU over a packed up-projection u[rows, ld_u]: gate = u[:, 0:width],
+ * value = u[:, width:2*width].  dtype is RV_F16 or RV_F32.
+ *   o[r, c] = round_dtype(silu(gate)) * value        (o is [rows, width])
+ * silu is computed in FP32 and rounded to the I/O dtype before the multiply.
+ * Replaces _swiglu_forward + FusedSwiGLU.forward
+ *   (src/reversibility/kernels.py:88-95, 113-122).
+ * ld_u >= 2*width.
+ */
+int rv_swiglu_fwd(const void* u, int64_t ld_u, void* o, int64_t rows,
+                  int64_t width, int dtype, void* stream);
+
+/* SwiGLU backward into the packed gradient du[rows, ld_u]:
+ *   s          = sigmoid(gate)
+ *   du[:, gate]  = round(dy * value) * (s * (1 + gate * (1 - s)))
+ *   du[:, value] = dy * round(gate * s)
+ * Columns of du beyond 2*width (if ld_u > 2*width) are left untouched.
+ * Replaces _swiglu_backward + FusedSwiGLU.backward
+ *   (src/reversibility/kernels.py:98-110, 124-131).
+ */
+int rv_swiglu_bwd(const void* u, int64_t ld_u, const void* dy, void* du,
+                  int64_t rows, int64_t width, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused midpoint residual update (paper Eq. 2.4/2.5):
+ *   f      = round_T(a + m)                  (attention + MLP terms)
+ *   out[i] = p[i] + sign * S(round_T(f * scale))
+ * with p/out in state dtype S (RV_F32 or RV_F64) and a, m in force dtype T
+ * (RV_F16, RV_BF16, RV_F32 or RV_F64, T no wider than S).  scale is 2*h.
+ * sign = +1 is forward_pair's p + 2h f(q); sign = -1 is inverse_pair's
+ * q - 2h f(p).  out may alias p.
+ * Replaces the eager residual arithmetic of midpoint_force/forward_pair/
+ * inverse_pair (src/reversibility/reversible.py:16-18, 21-24, 28-30).
+ */
+int rv_midpoint_update(const void* p, const void* a, const void* m, void* out,
+                       double scale, int sign, int64_t n, int state_dtype,
+                       int force_dtype, void* stream);
+
+/* Gradient of rv_midpoint_update with respect to a and m (both equal):
+ *   da[i] = round_T(round_T(dout[i]) * scale) * sign
+ * dout is in the state dtype, da in the force dtype.  (The gradient with
+ * respect to p is dout itself.)  Matches autograd through the eager
+ * expression, including the cast of the FP32 gradient to the force dtype.
+ */
+int rv_midpoint_update_bwd(const void* dout, void* da, double scale, int sign,
+                           int64_t n, int state_dtype, int force_dtype,
+                           void* stream);
+
+/* Hamiltonian-Euler residual update (paper Eq. 2.8/2.9):
+ *   out[i] = x[i] + sign * S(f[i])
+ * sign = +1: q + A(p), p + M(q');  sign = -1: p - M(q), q - A(p0).
+ * Replaces the eager adds of forward_pair/inverse_pair, Euler branch
+ *   (src/reversibility/reversible.py:24-25, 31-32).
+ */
+int rv_residual_axpy(const void* x, const void* f, void* out, int sign,
+                     int64_t n, int state_dtype, int force_dtype,
+                     void* stream);
+
+/* Fused residual add + RMSNorm (the x + A(x) -> mlp_norm step of
+ * midpoint_force and the q' = q + A(p) -> mlp_norm step of Euler):
+ *   h[r, :] = x[r, :] + S(f[r, :])             (written to h)
+ *   y, rstd = RMSNorm(h) as in rv_rmsnorm_fwd
+ * x, h, y: FP32; f: RV_F16, RV_BF16 or RV_F32.  h may alias x.
+ * Replaces the eager `x + attention` / `q + block.attn(...)` followed by
+ * block.mlp_norm (src/reversibility/reversible.py:17-18, 24-25;
+ * src/reversibility/kernels_v3.py:9-16).
+ */
+int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
+                       const float* w, float* h, float* y, float* rstd,
+                       int64_t rows, int64_t width, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REVERSIBILITY_HIP_H */

@@ -1,0 +1,525 @@
+// Fused RMSNorm forward/backward for gfx950.
+//
+// Layout: x, y, dy, dx are [rows, width] FP32 row-major; w and dw are
+// [width]; rstd is [rows].  One wavefront owns one row at a time: with
+// width = 256 each of the 64 lanes holds one float4 (16-byte loads, the whole
+// row is one 1 KiB coalesced access); wider rows use VEC float4 per lane.
+// Each wave keeps RPW rows in flight to cover HBM latency.
+//
+// Backward is a single pass over x and dy: every wave computes dx for its
+// rows and accumulates dy * (x * rstd) per column in registers; the waves of
+// a block combine through LDS and the block writes one partial row of dw
+// (stored column-major, [width][nparts]).  A second small kernel sums the
+// partials of each column in a fixed order, one wavefront per column.
+//
+// Arithmetic follows src/reversibility/kernels_v3.py:9-48 operation by
+// operation (sum/width + eps, x*r*w, g*x reduction, (g - x*c)*r, and the
+// forward multiply order x*r inside the dweight sum); the build disables FMA
+// contraction to match the reference's enable_fp_fusion=False.
+
+#include "rv_device.h"
+
+namespace {
+
+using rv::wave_sum;
+
+constexpr int kFwdWaves = 4;     // waves per block, forward
+constexpr int kBwdWaves = 8;     // waves per block, backward
+constexpr int kMaxVec = 16;      // float4 per lane => width <= 4096
+constexpr int kMaxEpl = 64;      // scalar path: elements per lane <= 64
+
+// ---------------------------------------------------------------------------
+// Forward, width % 4 == 0, width <= 256 * VEC.
+// With ADD the row input is x + float(f) (fused residual add) and that sum is
+// also written to h.
+// ---------------------------------------------------------------------------
+template <int VEC, int RPW, typename F, bool ADD>
+__global__ __launch_bounds__(kFwdWaves * 64)
+void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
+                 const float* __restrict__ w, float* __restrict__ h,
+                 float* __restrict__ y, float* __restrict__ rstd,
+                 int64_t rows, int width, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t base =
+      ((int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6)) * RPW;
+  if (base >= rows) return;  // wave-uniform
+
+  // w of a column >= width only meets outputs that are never stored, so it
+  // needs no masking here.
+  float4 wv[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const int col = (v * 64 + lane) * 4;
+    wv[v] = rv::ld_f4(w + (col < width ? col : width - 4));
+  }
+
+  // Issue every load of the RPW rows before any arithmetic.  Out-of-range
+  // rows/columns load from a clamped, valid address and are zeroed with a
+  // select, so the loads carry no branches (a branch would make the compiler
+  // wait for each row's loads before issuing the next row's).
+  float4 xv[RPW][VEC];
+  float4 fv[ADD ? RPW : 1][VEC];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = base + r;
+    const int64_t row_c = row < rows ? row : rows - 1;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int col = (v * 64 + lane) * 4;
+      const int col_c = col < width ? col : width - 4;
+      xv[r][v] = rv::ld_f4(x + row_c * width + col_c);
+      if constexpr (ADD) fv[r][v] = rv::load4f(f + row_c * width + col_c);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const bool ok = base + r < rows && (v * 64 + lane) * 4 < width;
+      xv[r][v] = rv::keep_if(xv[r][v], ok);
+      if constexpr (ADD) fv[r][v] = rv::keep_if(fv[r][v], ok);
+    }
+  if constexpr (ADD) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        xv[r][v].x = xv[r][v].x + fv[r][v].x;
+        xv[r][v].y = xv[r][v].y + fv[r][v].y;
+        xv[r][v].z = xv[r][v].z + fv[r][v].z;
+        xv[r][v].w = xv[r][v].w + fv[r][v].w;
+      }
+  }
+
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = base + r;
+    float ss = 0.f;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      ss = ss + xv[r][v].x * xv[r][v].x;
+      ss = ss + xv[r][v].y * xv[r][v].y;
+      ss = ss + xv[r][v].z * xv[r][v].z;
+      ss = ss + xv[r][v].w * xv[r][v].w;
+    }
+    ss = wave_sum(ss);
+    const float rs = rsqrtf(ss / (float)width + eps);
+    if (row < rows) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int col = (v * 64 + lane) * 4;
+        if (col < width) {
+          const float4 t = xv[r][v];
+          float4 o;
+          o.x = (t.x * rs) * wv[v].x;
+          o.y = (t.y * rs) * wv[v].y;
+          o.z = (t.z * rs) * wv[v].z;
+          o.w = (t.w * rs) * wv[v].w;
+          rv::st_f4(y + row * width + col, o);
+          if constexpr (ADD) rv::st_f4(h + row * width + col, t);
+        }
+      }
+      if (lane == 0) rstd[row] = rs;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward, any width <= 64 * EPL (scalar, element j of a lane is column
+// j*64 + lane).
+// ---------------------------------------------------------------------------
+template <int EPL, typename F, bool ADD>
+__global__ __launch_bounds__(kFwdWaves * 64)
+void rms_fwd_scalar(const float* __restrict__ x, const F* __restrict__ f,
+                    const float* __restrict__ w, float* __restrict__ h,
+                    float* __restrict__ y, float* __restrict__ rstd,
+                    int64_t rows, int width, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float xv[EPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int col = j * 64 + lane;
+    float t = 0.f;
+    if (col < width) {
+      t = x[row * width + col];
+      if constexpr (ADD) t = t + rv::Conv<F>::to_f(f[row * width + col]);
+    }
+    xv[j] = t;
+    ss = ss + t * t;
+  }
+  ss = wave_sum(ss);
+  const float rs = rsqrtf(ss / (float)width + eps);
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int col = j * 64 + lane;
+    if (col < width) {
+      y[row * width + col] = (xv[j] * rs) * w[col];
+      if constexpr (ADD) h[row * width + col] = xv[j];
+    }
+  }
+  if (lane == 0) rstd[row] = rs;
+}
+
+// ---------------------------------------------------------------------------
+// Backward, width % 4 == 0.  Block b owns rows [b*rpb, min((b+1)*rpb, rows)).
+// Wave k of the block handles rows start + k*2 + {0,1}, then strides by
+// 2*kBwdWaves.  Writes dx and the block's dw partial (column-major).
+// ---------------------------------------------------------------------------
+template <int VEC>
+__global__ __launch_bounds__(kBwdWaves * 64)
+void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
+                 const float* __restrict__ dy, const float* __restrict__ rstd,
+                 float* __restrict__ dx, float* __restrict__ partial,
+                 int64_t rows, int width, int64_t rows_per_block,
+                 int nparts) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t start = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t end = start + rows_per_block < rows ? start + rows_per_block : rows;
+
+  float4 wv[VEC];
+  float4 acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const int col = (v * 64 + lane) * 4;
+    wv[v] = rv::keep_if(rv::ld_f4(w + (col < width ? col : width - 4)),
+                        col < width);
+    acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float fwidth = (float)width;
+
+  for (int64_t row0 = start + 2 * wave; row0 < end; row0 += 2 * kBwdWaves) {
+    // Branch-free loads from clamped addresses, then zero what is out of
+    // range (see rms_fwd_vec).
+    float4 xv[2][VEC], gv[2][VEC];
+    float rs[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int64_t row = row0 + r < end ? row0 + r : end - 1;
+      rs[r] = rstd[row];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const int col = (v * 64 + lane) * 4;
+        const int col_c = col < width ? col : width - 4;
+        xv[r][v] = rv::ld_f4(x + row * width + col_c);
+        gv[r][v] = rv::ld_f4(dy + row * width + col_c);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      rs[r] = rv::keep_if(rs[r], row0 + r < end);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const bool ok = row0 + r < end && (v * 64 + lane) * 4 < width;
+        xv[r][v] = rv::keep_if(xv[r][v], ok);
+        gv[r][v] = rv::keep_if(gv[r][v], ok);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int64_t row = row0 + r;
+      float dot = 0.f;
+      float4 g[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        g[v].x = gv[r][v].x * wv[v].x;
+        g[v].y = gv[r][v].y * wv[v].y;
+        g[v].z = gv[r][v].z * wv[v].z;
+        g[v].w = gv[r][v].w * wv[v].w;
+        dot = dot + g[v].x * xv[r][v].x;
+        dot = dot + g[v].y * xv[r][v].y;
+        dot = dot + g[v].z * xv[r][v].z;
+        dot = dot + g[v].w * xv[r][v].w;
+      }
+      dot = wave_sum(dot);
+      const float c = ((dot / fwidth) * rs[r]) * rs[r];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const float4 t = xv[r][v];
+        // dweight partial: dy * (x * r), forward multiply order.
+        acc[v].x = acc[v].x + gv[r][v].x * (t.x * rs[r]);
+        acc[v].y = acc[v].y + gv[r][v].y * (t.y * rs[r]);
+        acc[v].z = acc[v].z + gv[r][v].z * (t.z * rs[r]);
+        acc[v].w = acc[v].w + gv[r][v].w * (t.w * rs[r]);
+        const int col = (v * 64 + lane) * 4;
+        if (row < end && col < width) {
+          float4 o;
+          o.x = (g[v].x - t.x * c) * rs[r];
+          o.y = (g[v].y - t.y * c) * rs[r];
+          o.z = (g[v].z - t.z * c) * rs[r];
+          o.w = (g[v].w - t.w * c) * rs[r];
+          rv::st_f4(dx + row * width + col, o);
+        }
+      }
+    }
+  }
+
+  // Combine the waves' column partials in wave order, at most 4 float4 per
+  // lane per pass.
+  constexpr int kPass = VEC < 4 ? VEC : 4;
+  __shared__ float4 red[kBwdWaves][kPass * 64];
+#pragma unroll
+  for (int v0 = 0; v0 < VEC; v0 += kPass) {
+#pragma unroll
+    for (int v = 0; v < kPass; ++v) red[wave][v * 64 + lane] = acc[v0 + v];
+    __syncthreads();
+    for (int s = threadIdx.x; s < kPass * 64; s += kBwdWaves * 64) {
+      float4 t = red[0][s];
+#pragma unroll
+      for (int k = 1; k < kBwdWaves; ++k) {
+        t.x = t.x + red[k][s].x;
+        t.y = t.y + red[k][s].y;
+        t.z = t.z + red[k][s].z;
+        t.w = t.w + red[k][s].w;
+      }
+      const int col = (v0 * 64 + s) * 4;
+      if (col < width) {
+        partial[(int64_t)(col + 0) * nparts + blockIdx.x] = t.x;
+        partial[(int64_t)(col + 1) * nparts + blockIdx.x] = t.y;
+        partial[(int64_t)(col + 2) * nparts + blockIdx.x] = t.z;
+        partial[(int64_t)(col + 3) * nparts + blockIdx.x] = t.w;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, any width <= 64 * EPL (scalar).  Same structure as the vector
+// kernel; element j of a lane is column j*64 + lane.
+// ---------------------------------------------------------------------------
+template <int EPL>
+__global__ __launch_bounds__(kBwdWaves * 64)
+void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
+                    const float* __restrict__ dy, const float* __restrict__ rstd,
+                    float* __restrict__ dx, float* __restrict__ partial,
+                    int64_t rows, int width, int64_t rows_per_block,
+                    int nparts) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t start = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t end = start + rows_per_block < rows ? start + rows_per_block : rows;
+  float wv[EPL], acc[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int col = j * 64 + lane;
+    wv[j] = col < width ? w[col] : 0.f;
+    acc[j] = 0.f;
+  }
+  for (int64_t row = start + wave; row < end; row += kBwdWaves) {
+    const float rs = rstd[row];
+    float xv[EPL], gv[EPL], g[EPL];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int col = j * 64 + lane;
+      xv[j] = col < width ? x[row * width + col] : 0.f;
+      gv[j] = col < width ? dy[row * width + col] : 0.f;
+      g[j] = gv[j] * wv[j];
+      dot = dot + g[j] * xv[j];
+    }
+    dot = wave_sum(dot);
+    const float c = ((dot / (float)width) * rs) * rs;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int col = j * 64 + lane;
+      acc[j] = acc[j] + gv[j] * (xv[j] * rs);
+      if (col < width) dx[row * width + col] = (g[j] - xv[j] * c) * rs;
+    }
+  }
+  __shared__ float red[kBwdWaves][64];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    red[wave][lane] = acc[j];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      float t = red[0][threadIdx.x];
+#pragma unroll
+      for (int k = 1; k < kBwdWaves; ++k) t = t + red[k][threadIdx.x];
+      const int col = j * 64 + threadIdx.x;
+      if (col < width) partial[(int64_t)col * nparts + blockIdx.x] = t;
+    }
+    __syncthreads();
+  }
+}
+
+// dw[col] = sum over parts of partial[col][part]; one wavefront per column,
+// lane l sums parts l, l+64, ... in order, then a fixed-order wave sum.
+__global__ __launch_bounds__(256)
+void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
+                   int width, int nparts) {
+  const int lane = threadIdx.x & 63;
+  const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (col >= width) return;
+  const float* p = partial + (int64_t)col * nparts;
+  float s = 0.f;
+#pragma unroll 8
+  for (int i = lane; i < nparts; i += 64) s = s + p[i];
+  s = wave_sum(s);
+  if (lane == 0) dw[col] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Launch plumbing
+// ---------------------------------------------------------------------------
+struct BwdPlan {
+  int64_t rows_per_block;
+  int nparts;
+};
+
+// 512 blocks = two per compute unit on a 256-CU MI355X, all resident at
+// once, every block with the same number of rows (no partial second wave of
+// blocks).  The count is a constant, not a device query, so the dw summation
+// order -- and therefore dw bit for bit -- does not depend on the device.
+constexpr int64_t kBwdTargetBlocks = 512;
+
+BwdPlan plan_bwd(int64_t rows) {
+  const int64_t target = kBwdTargetBlocks;
+  int64_t rpb = (rows + target - 1) / target;
+  if (rpb < 1) rpb = 1;
+  BwdPlan p;
+  p.rows_per_block = rpb;
+  p.nparts = (int)((rows + rpb - 1) / rpb);
+  return p;
+}
+
+template <typename F, bool ADD>
+int launch_fwd(const float* x, const F* f, const float* w, float* h, float* y,
+               float* rstd, int64_t rows, int width, float eps,
+               hipStream_t stream) {
+  const bool vec = (width % 4 == 0) && rv_host::aligned16(x) &&
+                   rv_host::aligned16(w) && rv_host::aligned16(y) &&
+                   (h == nullptr || rv_host::aligned16(h)) &&
+                   (f == nullptr ||
+                    (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0);
+  if (vec && width <= 256 * kMaxVec) {
+    constexpr int RPW = 2;
+    const int64_t rows_per_block = (int64_t)kFwdWaves * RPW;
+    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+    const dim3 block(kFwdWaves * 64);
+    const int vecs = (width + 255) / 256;
+#define RV_FWD_VEC(V)                                                          \
+  hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, ADD>), grid, block, 0, stream, x, f, \
+                     w, h, y, rstd, rows, width, eps)
+    if (vecs <= 1) RV_FWD_VEC(1);
+    else if (vecs <= 2) RV_FWD_VEC(2);
+    else if (vecs <= 4) RV_FWD_VEC(4);
+    else if (vecs <= 8) RV_FWD_VEC(8);
+    else RV_FWD_VEC(16);
+#undef RV_FWD_VEC
+    return rv_host::check_launch();
+  }
+  if (width > 64 * kMaxEpl) return RV_ERR_UNSUPPORTED;
+  const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
+  const dim3 block(kFwdWaves * 64);
+  const int epl = (width + 63) / 64;
+#define RV_FWD_SC(E)                                                         \
+  hipLaunchKernelGGL((rms_fwd_scalar<E, F, ADD>), grid, block, 0, stream, x, f, w, \
+                     h, y, rstd, rows, width, eps)
+  if (epl <= 1) RV_FWD_SC(1);
+  else if (epl <= 2) RV_FWD_SC(2);
+  else if (epl <= 4) RV_FWD_SC(4);
+  else if (epl <= 8) RV_FWD_SC(8);
+  else if (epl <= 16) RV_FWD_SC(16);
+  else if (epl <= 32) RV_FWD_SC(32);
+  else RV_FWD_SC(64);
+#undef RV_FWD_SC
+  return rv_host::check_launch();
+}
+
+}  // namespace
+
+extern "C" {
+
+int rv_rmsnorm_fwd(const float* x, const float* w, float* y, float* rstd,
+                   int64_t rows, int64_t width, float eps, void* stream) {
+  if (!x || !w || !y || !rstd) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096) return RV_ERR_UNSUPPORTED;
+  return launch_fwd<float, false>(x, nullptr, w, nullptr, y, rstd, rows,
+                                  (int)width, eps, (hipStream_t)stream);
+}
+
+int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
+                       const float* w, float* h, float* y, float* rstd,
+                       int64_t rows, int64_t width, float eps, void* stream) {
+  if (!x || !f || !w || !h || !y || !rstd) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096) return RV_ERR_UNSUPPORTED;
+  const hipStream_t s = (hipStream_t)stream;
+  switch (force_dtype) {
+    case RV_F32:
+      return launch_fwd<float, true>(x, (const float*)f, w, h, y, rstd, rows,
+                                     (int)width, eps, s);
+    case RV_F16:
+      return launch_fwd<__half, true>(x, (const __half*)f, w, h, y, rstd,
+                                      rows, (int)width, eps, s);
+    case RV_BF16:
+      return launch_fwd<__hip_bfloat16, true>(x, (const __hip_bfloat16*)f, w,
+                                              h, y, rstd, rows, (int)width,
+                                              eps, s);
+    default:
+      return RV_ERR_UNSUPPORTED;
+  }
+}
+
+int64_t rv_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t width) {
+  if (rows <= 0 || width <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
+  const BwdPlan p = plan_bwd(rows);
+  return (int64_t)p.nparts * width * (int64_t)sizeof(float);
+}
+
+int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
+                   const float* rstd, float* dx, float* dw, void* workspace,
+                   int64_t workspace_bytes, int64_t rows, int64_t width,
+                   void* stream) {
+  if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096) return RV_ERR_UNSUPPORTED;
+  const BwdPlan p = plan_bwd(rows);
+  const int64_t need = (int64_t)p.nparts * width * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
+  float* partial = (float*)workspace;
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)p.nparts);
+  const dim3 block(kBwdWaves * 64);
+  const int iw = (int)width;
+  const bool vec = (width % 4 == 0) && rv_host::aligned16(x) &&
+                   rv_host::aligned16(w) && rv_host::aligned16(dy) &&
+                   rv_host::aligned16(dx);
+  if (vec) {
+    const int vecs = (iw + 255) / 256;
+#define RV_BWD_VEC(V)                                                       \
+  hipLaunchKernelGGL((rms_bwd_vec<V>), grid, block, 0, s, x, w, dy, rstd, dx, \
+                     partial, rows, iw, p.rows_per_block, p.nparts)
+    if (vecs <= 1) RV_BWD_VEC(1);
+    else if (vecs <= 2) RV_BWD_VEC(2);
+    else if (vecs <= 4) RV_BWD_VEC(4);
+    else if (vecs <= 8) RV_BWD_VEC(8);
+    else RV_BWD_VEC(16);
+#undef RV_BWD_VEC
+  } else {
+    const int epl = (iw + 63) / 64;
+#define RV_BWD_SC(E)                                                          \
+  hipLaunchKernelGGL((rms_bwd_scalar<E>), grid, block, 0, s, x, w, dy, rstd, dx, \
+                     partial, rows, iw, p.rows_per_block, p.nparts)
+    if (epl <= 1) RV_BWD_SC(1);
+    else if (epl <= 2) RV_BWD_SC(2);
+    else if (epl <= 4) RV_BWD_SC(4);
+    else if (epl <= 8) RV_BWD_SC(8);
+    else if (epl <= 16) RV_BWD_SC(16);
+    else if (epl <= 32) RV_BWD_SC(32);
+    else RV_BWD_SC(64);
+#undef RV_BWD_SC
+  }
+  int st = rv_host::check_launch();
+  if (st != RV_OK) return st;
+  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 3) / 4)), dim3(256),
+                     0, s, partial, dw, iw, p.nparts);
+  return rv_host::check_launch();
+}
+
+}  // extern "C"

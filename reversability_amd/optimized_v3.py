@@ -1,0 +1,265 @@
+"""Per-layer workspace reduction: token-tiled MLP and split midpoint backward.
+
+Restates src/reversibility/optimized_v3.py:10-192.
+
+``TiledMLP`` saves only the normalized input and the two weights and
+recomputes bounded token tiles in backward.  Its backward is written out
+(instead of rebuilding an autograd graph per tile and calling
+``autograd.grad``): per tile it recomputes ``u = x W_up^T`` and ``o = swiglu(u)``
+-- the down projection output is not needed for gradients and is not
+recomputed -- then
+
+    d_o    = dy W_down          dW_down += fp32(dy^T o)
+    du     = swiglu_bwd(u, d_o)
+    dx     = fp32(du W_up)      dW_up   += fp32(du^T x)
+
+with the same casts autocast's ``F.linear`` applies (inputs and weights to the
+autocast dtype; gradients of fp32 leaves cast back to fp32) and the same
+per-tile fp32 accumulation order as the reference's ``add_``.
+"""
+from __future__ import annotations
+
+import types
+
+import torch
+import torch.nn.functional as F
+from torch.autograd.function import once_differentiable
+
+from .optimized import ReusedMidpoint, amp_context, hidden_states
+from .residual import midpoint_step
+
+
+def mlp_value(x, up, down, fused):
+    """down(swiglu(x up^T)) under the caller's autocast (optimized_v3.py:10-18)."""
+    u = F.linear(x, up)
+    if fused:
+        from .kernels import FusedSwiGLU
+        value = FusedSwiGLU.apply(u)
+    else:
+        gate, value = u.chunk(2, -1)
+        value = F.silu(gate) * value
+    return F.linear(value, down)
+
+
+def _swiglu_forward(u, fused):
+    if fused:
+        from .kernels import _validate
+        from ._hip import ops
+        _validate(u)
+        return ops.swiglu_fwd(u)
+    gate, value = u.chunk(2, -1)
+    return F.silu(gate) * value
+
+
+def _swiglu_backward(u, d_o, fused):
+    if fused:
+        from ._hip import ops
+        return ops.swiglu_bwd(u, d_o.contiguous())
+    with torch.enable_grad():
+        leaf = u.detach().requires_grad_(True)
+        gate, value = leaf.chunk(2, -1)
+        out = F.silu(gate) * value
+        du, = torch.autograd.grad(out, leaf, d_o)
+    return du
+
+
+def tile_forward(x, up, down, fused, compute_dtype, need_output=True):
+    """One tile of the MLP in ``compute_dtype``: returns (x_c, up_c, u, o, y)."""
+    x_c = x.to(compute_dtype)
+    up_c = up.to(compute_dtype)
+    u = torch.mm(x_c, up_c.t())
+    o = _swiglu_forward(u, fused)
+    y = torch.mm(o, down.to(compute_dtype).t()) if need_output else None
+    return x_c, up_c, u, o, y
+
+
+def _compute_dtype(x, amp, amp_dtype):
+    if amp and x.dtype == torch.float32:
+        return amp_dtype
+    return x.dtype
+
+
+class TiledMLP(torch.autograd.Function):
+    """Save only the normalized input and weights; recompute token tiles in backward.
+
+    Attention still sees all sequences; each optimizer update consumes one whole
+    physical batch.  Parameter gradients return through autograd inputs.
+    """
+
+    @staticmethod
+    def forward(ctx, x, up, down, tokens, fused):
+        if tokens < 1:
+            raise ValueError("Positive MLP tile size required")
+        ctx.tokens, ctx.fused = tokens, fused
+        ctx.device = x.device.type
+        ctx.amp = torch.is_autocast_enabled(ctx.device)
+        ctx.dtype = torch.get_autocast_dtype(ctx.device)
+        cdt = _compute_dtype(x, ctx.amp, ctx.dtype)
+        flat = x.reshape(-1, x.shape[-1])
+        output = torch.empty((flat.shape[0], down.shape[0]), device=x.device, dtype=cdt)
+        with torch.autocast(ctx.device, enabled=False):
+            for start in range(0, flat.shape[0], tokens):
+                *_, y = tile_forward(flat[start:start + tokens], up, down, fused, cdt)
+                output[start:start + tokens].copy_(y)
+        ctx.save_for_backward(x, up, down)
+        return output.reshape(*x.shape[:-1], down.shape[0])
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gradient):
+        x, up, down = ctx.saved_tensors
+        cdt = _compute_dtype(x, ctx.amp, ctx.dtype)
+        flat = x.reshape(-1, x.shape[-1])
+        dy = gradient.reshape(-1, gradient.shape[-1]).to(cdt)
+        dx = torch.empty_like(flat)
+        dup = torch.zeros_like(up)
+        ddown = torch.zeros_like(down)
+        down_c = down.to(cdt)
+        with torch.autocast(ctx.device, enabled=False):
+            for start in range(0, flat.shape[0], ctx.tokens):
+                stop = start + ctx.tokens
+                x_c, up_c, u, o, _ = tile_forward(flat[start:stop], up, down, ctx.fused, cdt,
+                                                  need_output=False)
+                g = dy[start:stop]
+                d_o = torch.mm(g, down_c)
+                ddown.add_(torch.mm(g.t(), o).to(down.dtype))
+                du = _swiglu_backward(u, d_o, ctx.fused)
+                dx[start:stop].copy_(torch.mm(du, up_c))
+                dup.add_(torch.mm(du.t(), x_c).to(up.dtype))
+                del x_c, up_c, u, o, g, d_o, du
+        return dx.reshape_as(x), dup, ddown, None, None
+
+
+class SplitMidpoint(torch.autograd.Function):
+    """MLP VJP first, then attention recompute + VJP (optimized_v3.py:66-117).
+
+    A detached attention proxy carries the force's dependence on attention, so
+    the MLP graph can be released before attention is rebuilt.  Attention is
+    recomputed (the disclosed extra-compute trade-off).
+    """
+
+    @staticmethod
+    def forward(ctx, p, q, blocks, h, *parameters):
+        ctx.blocks, ctx.h = blocks, h
+        ctx.device = p.device.type
+        ctx.amp = torch.is_autocast_enabled(ctx.device)
+        ctx.dtype = torch.get_autocast_dtype(ctx.device)
+        from .reversible import forward_pair
+        for block in blocks:
+            p, q = forward_pair(block, p, q, "midpoint", h)
+        ctx.save_for_backward(p, q, *parameters)
+        return p, q
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dp, dq):
+        p, q, *_ = ctx.saved_tensors
+        grads: list = []
+        scale = 2 * ctx.h
+        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype):
+            for block in reversed(ctx.blocks):
+                with torch.no_grad():
+                    attention = block.attn(block.attn_norm(p))
+                with torch.enable_grad():
+                    previous_q = p.detach().requires_grad_(True)
+                    proxy = attention.detach().requires_grad_(True)
+                    mlp = block.mlp(block.mlp_norm(previous_q + proxy))
+                    with torch.no_grad():
+                        previous_p = midpoint_step(q, proxy.detach(), mlp.detach(), scale, -1)
+                    previous_p.requires_grad_(True)
+                    next_q = midpoint_step(previous_p, proxy, mlp, scale, +1)
+                    mlp_parameters = (*block.mlp_norm.parameters(), *block.mlp.parameters())
+                    local = torch.autograd.grad((previous_q, next_q),
+                                                (previous_p, previous_q, proxy, *mlp_parameters),
+                                                (dp, dq))
+                next_dp, q_mlp, attention_cotangent = local[:3]
+                mlp_grads = local[3:]
+                del attention, proxy, mlp, next_q, local
+                with torch.enable_grad():
+                    attn_input = previous_q.detach().requires_grad_(True)
+                    attention = block.attn(block.attn_norm(attn_input))
+                    attention_parameters = (*block.attn_norm.parameters(), *block.attn.parameters())
+                    attn_local = torch.autograd.grad(attention, (attn_input, *attention_parameters),
+                                                     attention_cotangent)
+                dp, dq = next_dp, q_mlp + attn_local[0]
+                by_id = {id(w): g for w, g in zip((*attention_parameters, *mlp_parameters),
+                                                  (*attn_local[1:], *mlp_grads))}
+                grads[0:0] = [by_id[id(w)] for w in block.parameters()]
+                p, q = previous_p.detach(), previous_q.detach()
+                del attn_input, attention, attn_local, attention_cotangent, q_mlp, by_id, mlp_grads
+        return (dp, dq, None, None, *grads)
+
+
+def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsnorm=False):
+    """Wire the optimized core, tiled MLP, fused SwiGLU and fused RMSNorm
+    (optimized_v3.py:120-148).  Idempotent for one configuration; raises on a
+    conflicting reinstall, a non-midpoint optimized core, or a biased MLP."""
+    signature = (core_mode, mlp_tokens, swiglu, rmsnorm)
+    if hasattr(model, "_v3_signature"):
+        if model._v3_signature != signature:
+            raise ValueError("Cannot replace an installed v3 configuration")
+        return model
+    if core_mode != "reference":
+        if getattr(model, "method", None) != "midpoint" or model.backward_mode != "reconstruct":
+            raise ValueError("Optimized core requires reconstructed midpoint")
+        core_function = {"reuse": ReusedMidpoint, "split": SplitMidpoint}[core_mode]
+
+        def core(self, x):
+            _, y = core_function.apply(x, x, self.blocks, self.step_size, *self.blocks.parameters())
+            return y
+        model.core = types.MethodType(core, model)
+    if mlp_tokens:
+        for block in model.blocks:
+            if block.mlp.up.bias is not None or block.mlp.down.bias is not None:
+                raise ValueError("Tiled MLP experiment supports frozen bias=False only")
+
+            def forward(self, x):
+                return TiledMLP.apply(x, self.up.weight, self.down.weight, mlp_tokens, swiglu)
+            block.mlp.forward = types.MethodType(forward, block.mlp)
+    elif swiglu:
+        from .kernels import enable_swiglu
+        enable_swiglu(model)
+    if rmsnorm:
+        from .kernels_v3 import enable_rmsnorm
+        enable_rmsnorm(model)
+    model._v3_signature = signature
+    return model
+
+
+def cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler=None,
+                         precision="fp32", reuse=False, loss_backend="torch"):
+    """Chunked tied-head loss with one head-weight cast per update
+    (optimized_v3.py:151-192).  Each chunk's head gradient is promoted to the
+    weight dtype before it is added to the tied ``.grad``."""
+    if reuse or chunk_tokens < 1 or denominator < 1:
+        raise ValueError("Use installed core mode and positive normalization/chunk")
+    with amp_context(ids.device, precision):
+        hidden = hidden_states(model, ids)
+    leaf = hidden.detach().reshape(-1, hidden.shape[-1]).requires_grad_(True)
+    weight = model.lm_head.weight
+    if ids.device.type != "cuda" or precision == "fp32":
+        dtype = weight.dtype
+    else:
+        dtype = {"fp16": torch.float16, "bf16": torch.bfloat16}[precision]
+    head = weight.detach().to(dtype).requires_grad_(True)
+    targets = labels.reshape(-1)
+    total = torch.zeros((), device=ids.device, dtype=torch.float32)
+    from .optimized import _chunk_loss
+    for start in range(0, targets.numel(), chunk_tokens):
+        with amp_context(ids.device, precision, cache=False):
+            logits = F.linear(leaf[start:start + chunk_tokens], head)
+            loss = _chunk_loss(logits, targets[start:start + chunk_tokens], loss_backend)
+            normalized = loss / denominator
+            (normalized if scaler is None else scaler.scale(normalized)).backward()
+        chunk_grad = head.grad.detach().to(weight.dtype)
+        if weight.grad is None:
+            weight.grad = chunk_grad
+        else:
+            weight.grad.add_(chunk_grad)
+        head.grad = None
+        total += loss.detach().float()
+        del logits, loss, normalized, chunk_grad
+    del head
+    with amp_context(ids.device, precision):
+        hidden.backward(leaf.grad.reshape_as(hidden))
+    return total

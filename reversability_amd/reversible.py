@@ -1,0 +1,138 @@
+"""Reversible integrators and the stack-level reconstruction backward.
+
+Restates src/reversibility/reversible.py:16-118 (paper Eq. 2.4/2.5 midpoint,
+Eq. 2.8/2.9 Hamiltonian Euler):
+
+* midpoint:  (p, q) -> (q, p + 2h f(q)),   f(x) = A(x) + M(x + A(x)),
+  inverse    (p, q) -> (q - 2h f(p), p);
+* Euler:     q' = q + A(p), p' = p + M(q');  inverse p = p' - M(q'), q = q' - A(p);
+  A = attn . attn_norm, M = mlp . mlp_norm.
+
+``_InverseStack`` keeps only the final pair and parameter references; its
+backward walks the layers in reverse, reconstructs each layer's input under
+no_grad, rebuilds that one layer's graph with the forward's autocast mode and
+takes its VJP.  Parameter gradients are returned through autograd (never
+written to ``.grad``).  On ROCm tensors the residual updates run as fused HIP
+kernels (``residual.midpoint_step`` / ``residual.euler_step``) with the eager
+expression's rounding points.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from .model import BaselineLM, Block, ModelConfig
+from .residual import euler_step, midpoint_step
+
+
+def midpoint_terms(block: Block, x: torch.Tensor):
+    """(A(x), M(x + A(x))) -- the two summands of the midpoint force."""
+    attention = block.attn(block.attn_norm(x))
+    return attention, block.mlp(block.mlp_norm(x + attention))
+
+
+def midpoint_force(block: Block, x: torch.Tensor) -> torch.Tensor:
+    """f(x) = A(x) + M(x + A(x))  (reversible.py:16-18)."""
+    attention, mlp = midpoint_terms(block, x)
+    return attention + mlp
+
+
+def forward_pair(block, p, q, method, h):
+    """One integrator step (reversible.py:21-25)."""
+    if method == "midpoint":
+        attention, mlp = midpoint_terms(block, q)
+        return q, midpoint_step(p, attention, mlp, 2 * h, +1)
+    next_q = euler_step(q, block.attn(block.attn_norm(p)), +1)
+    return euler_step(p, block.mlp(block.mlp_norm(next_q)), +1), next_q
+
+
+def inverse_pair(block, p, q, method, h):
+    """Algebraic inverse of forward_pair (reversible.py:28-32)."""
+    if method == "midpoint":
+        attention, mlp = midpoint_terms(block, p)
+        return midpoint_step(q, attention, mlp, 2 * h, -1), p
+    previous_p = euler_step(p, block.mlp(block.mlp_norm(q)), -1)
+    return previous_p, euler_step(q, block.attn(block.attn_norm(previous_p)), -1)
+
+
+class _InverseStack(torch.autograd.Function):
+    """Whole-stack Function; backward reconstructs inputs layer by layer."""
+
+    @staticmethod
+    def forward(ctx, p, q, blocks, method, h, *parameters):
+        ctx.blocks, ctx.method, ctx.h = blocks, method, h
+        ctx.device_type = p.device.type
+        ctx.amp_enabled = torch.is_autocast_enabled(ctx.device_type)
+        ctx.amp_dtype = torch.get_autocast_dtype(ctx.device_type)
+        for block in blocks:
+            p, q = forward_pair(block, p, q, method, h)
+        ctx.save_for_backward(p, q, *parameters)
+        return p, q
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dp, dq):
+        p, q, *_ = ctx.saved_tensors
+        grads: list = []
+        with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype):
+            for block in reversed(ctx.blocks):
+                with torch.no_grad():
+                    p0, q0 = inverse_pair(block, p, q, ctx.method, ctx.h)
+                with torch.enable_grad():
+                    p0 = p0.detach().requires_grad_(True)
+                    q0 = q0.detach().requires_grad_(True)
+                    next_p, next_q = forward_pair(block, p0, q0, ctx.method, ctx.h)
+                    local = torch.autograd.grad((next_p, next_q), (p0, q0, *block.parameters()),
+                                                (dp, dq))
+                dp, dq = local[0], local[1]
+                grads[0:0] = local[2:]
+                p, q = p0.detach(), q0.detach()
+        return (dp, dq, None, None, None, *grads)
+
+
+class ReversibleLM(BaselineLM):
+    """BaselineLM whose block stack is a reversible integrator (reversible.py:72-107)."""
+
+    def __init__(self, config: ModelConfig, method: str, step_size: float = 0.5,
+                 backward_mode: str = "reconstruct") -> None:
+        if method not in {"midpoint", "euler"}:
+            raise ValueError("method must be midpoint or euler")
+        if not math.isfinite(step_size) or step_size <= 0:
+            raise ValueError("step size must be finite and positive")
+        if method == "euler" and step_size != 0.5:
+            raise ValueError("Euler has unit coefficients; step_size applies only to midpoint")
+        if backward_mode not in {"reconstruct", "autograd"}:
+            raise ValueError("unsupported backward mode")
+        if config.dropout != 0:
+            raise ValueError("reconstruction requires dropout=0; RNG replay is not implemented")
+        super().__init__(config)
+        self.method, self.step_size, self.backward_mode = method, step_size, backward_mode
+
+    def core(self, x):
+        # Boundary: p = q = embedding for both integrators.  The head reads q
+        # (midpoint) or p (Euler).
+        p = q = x
+        if self.backward_mode == "reconstruct" and torch.is_grad_enabled():
+            p, q = _InverseStack.apply(p, q, self.blocks, self.method, self.step_size,
+                                       *self.blocks.parameters())
+        else:
+            for block in self.blocks:
+                p, q = forward_pair(block, p, q, self.method, self.step_size)
+        return q if self.method == "midpoint" else p
+
+    def forward(self, input_ids):
+        return self.lm_head(self.final_norm(self.core(self.embed(input_ids))))
+
+
+def build_model(config: dict):
+    """Model factory over a study config dict (reversible.py:110-118)."""
+    model_config = ModelConfig(**config["model"])
+    method = config.get("method", "baseline")
+    if method == "baseline":
+        return BaselineLM(model_config)
+    if config.get("compile"):
+        raise ValueError("compiled inverse backward is not validated")
+    return ReversibleLM(model_config, method, config.get("step_size", 0.5),
+                        config.get("backward_mode", "reconstruct"))

@@ -1,0 +1,71 @@
+"""The C-ABI library: it loads, exports every entry point include/*.h declares,
+and rejects bad arguments with the documented status codes before touching a
+device (no kernel is launched here)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from reversability_amd import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions() -> list[str]:
+    names = []
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"\b(rv_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ["rv_rmsnorm_fwd", "rv_rmsnorm_bwd", "rv_rmsnorm_bwd_workspace_bytes",
+                     "rv_swiglu_fwd", "rv_swiglu_bwd", "rv_midpoint_update",
+                     "rv_midpoint_update_bwd", "rv_residual_axpy", "rv_add_rmsnorm_fwd"]:
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.library()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding declares a signature for each of them
+    assert set(declared_functions()) <= set(_hip.SIGNATURES)
+
+
+def test_status_strings_and_version():
+    lib = _hip.library()
+    assert lib.rv_abi_version() == _hip.ABI_VERSION
+    assert lib.rv_status_string(0) == b"ok"
+    for code in range(1, 6):
+        assert lib.rv_status_string(code) not in (b"ok", b"unknown status")
+
+
+def test_argument_validation_without_device():
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    assert lib.rv_rmsnorm_fwd(None, fake, fake, fake, 4, 256, 1e-7, None) == 1
+    assert lib.rv_rmsnorm_fwd(fake, fake, fake, fake, 0, 256, 1e-7, None) == 2
+    assert lib.rv_rmsnorm_fwd(fake, fake, fake, fake, 4, 8192, 1e-7, None) == 3
+    assert lib.rv_rmsnorm_bwd(fake, fake, fake, fake, fake, fake, fake, 0, 4, 256, None) == 4
+    assert lib.rv_rmsnorm_bwd(fake, fake, fake, fake, fake, fake, None, 1 << 20, 4, 256, None) == 4
+    assert lib.rv_swiglu_fwd(fake, 10, fake, 4, 8, _hip.RV_F16, None) == 2  # ld < 2*width
+    assert lib.rv_swiglu_fwd(fake, 16, fake, 4, 8, _hip.RV_F64, None) == 3
+    assert lib.rv_swiglu_bwd(None, 16, fake, fake, 4, 8, _hip.RV_F16, None) == 1
+    assert lib.rv_midpoint_update(fake, fake, fake, fake, 1.0, 2, 16, 0, 1, None) == 2
+    assert lib.rv_midpoint_update(fake, fake, fake, fake, 1.0, 1, 16, _hip.RV_F16, _hip.RV_F32, None) == 3
+    assert lib.rv_residual_axpy(fake, fake, fake, 1, -1, 0, 1, None) == 2
+    assert lib.rv_add_rmsnorm_fwd(fake, fake, _hip.RV_F64, fake, fake, fake, fake, 4, 256, 1e-7, None) == 3
+
+
+@pytest.mark.parametrize("rows,width", [(1, 8), (14848, 256), (32768, 1024), (69, 33)])
+def test_workspace_size_is_device_independent(rows, width):
+    n = _hip.rmsnorm_workspace_bytes(rows, width)
+    parts = -(-rows // -(-rows // 512))
+    assert n == parts * width * 4

@@ -1,0 +1,305 @@
+"""Pin the CPU oracle before any GPU result is compared against it.
+
+Every oracle function is checked against something it does not share code
+with: a library routine (torch's rms_norm / silu / eager fp16 arithmetic /
+autograd, numpy's float16 cast), a closed form or invariant, or brute force
+on tiny inputs -- chosen so that a dropped term, a wrong sign or index, or a
+wrong rounding point fails.  The committed golden file pins the oracle
+against drift.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+EPS32 = float(torch.finfo(torch.float32).eps)
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rng(seed=1337):
+    return np.random.default_rng(seed)
+
+
+# --------------------------------------------------------------------------
+# binary16 conversion
+# --------------------------------------------------------------------------
+
+def test_f16_all_patterns_roundtrip_and_match_numpy():
+    bits = np.arange(65536, dtype=np.uint16)
+    ours = oracle.f16_bits_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    back = oracle.f32_to_f16_bits(ours[~nan])
+    assert np.array_equal(back, bits[~nan])
+
+
+def test_f32_to_f16_rounding_matches_numpy():
+    r = rng()
+    # magnitudes across normal, subnormal, underflow and overflow ranges
+    vals = np.concatenate([
+        r.standard_normal(1 << 18).astype(np.float32),
+        (r.standard_normal(1 << 18) * 1e-5).astype(np.float32),
+        (r.standard_normal(1 << 17) * 1e-7).astype(np.float32),
+        (r.standard_normal(1 << 17) * 7e4).astype(np.float32),
+        r.integers(0, 1 << 32, 1 << 18, dtype=np.uint64).astype(np.uint32).view(np.float32),
+    ])
+    vals = vals[~np.isnan(vals)]
+    # exact halfway cases between adjacent binary16 values
+    h = np.arange(0, 0x7bff, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)
+    vals = np.concatenate([vals, mid, -mid])
+    ours = oracle.f32_to_f16_bits(vals)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+# --------------------------------------------------------------------------
+# RMSNorm
+# --------------------------------------------------------------------------
+
+def _rms_inputs(rows, width, seed=1337):
+    r = rng(seed)
+    x = r.standard_normal((rows, width)).astype(np.float32)
+    w = (1 + 0.02 * r.standard_normal(width)).astype(np.float32)
+    dy = r.standard_normal((rows, width)).astype(np.float32)
+    return x, w, dy
+
+
+@pytest.mark.parametrize("rows,width", [(69, 256), (17, 8), (5, 1024), (3, 33)])
+def test_rmsnorm_matches_torch_fp64(rows, width):
+    x, w, dy = _rms_inputs(rows, width)
+    y, rstd = oracle.rmsnorm_fwd(x, w, EPS32)
+    dx, dw = oracle.rmsnorm_bwd(x, w, dy, EPS32)
+    xt = torch.from_numpy(x).double().requires_grad_(True)
+    wt = torch.from_numpy(w).double().requires_grad_(True)
+    yt = F.rms_norm(xt, (width,), wt, eps=EPS32)
+    yt.backward(torch.from_numpy(dy).double())
+    # outputs are the fp64 values rounded once to fp32
+    np.testing.assert_allclose(y, yt.detach().numpy(), rtol=2e-7, atol=1e-30)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=2e-6, atol=2e-7)
+    np.testing.assert_allclose(dw, wt.grad.numpy(), rtol=2e-6, atol=2e-6)
+    ref_rstd = 1 / np.sqrt((x.astype(np.float64) ** 2).mean(-1) + EPS32)
+    np.testing.assert_allclose(rstd, ref_rstd, rtol=1e-7)
+
+
+def test_rmsnorm_scale_invariance_identity():
+    # With eps = 0, RMSNorm(x) is invariant to x -> a x, so <dx, x> = 0 per row.
+    x, w, dy = _rms_inputs(64, 256, seed=7)
+    dx, _ = oracle.rmsnorm_bwd(x, w, dy, 0.0)
+    dots = (dx.astype(np.float64) * x).sum(-1)
+    scale = np.linalg.norm(dx, axis=-1) * np.linalg.norm(x, axis=-1)
+    assert np.all(np.abs(dots) <= 1e-6 * scale)
+    # ... and a planted mistake (dropping the correction term) breaks it
+    dropped = (dy * w) * (1 / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True)))
+    bad = np.abs((dropped * x).sum(-1)) / (np.linalg.norm(dropped, axis=-1) * np.linalg.norm(x, axis=-1))
+    assert (bad > 1e-4).mean() > 0.9
+
+
+def test_rmsnorm_constant_row_closed_form():
+    width = 256
+    c = np.array([3.0, -0.5, 1e-3, 0.0], np.float32)
+    x = np.repeat(c[:, None], width, 1).astype(np.float32)
+    w = np.linspace(0.5, 1.5, width).astype(np.float32)
+    y, rstd = oracle.rmsnorm_fwd(x, w, EPS32)
+    expect = (c.astype(np.float64)[:, None] / np.sqrt(c.astype(np.float64)[:, None] ** 2 + EPS32)) * w
+    np.testing.assert_allclose(y, expect, rtol=1e-7, atol=0)
+    assert np.isfinite(rstd).all()
+
+
+def test_rmsnorm_finite_differences():
+    x, w, dy = _rms_inputs(3, 8, seed=3)
+    dx, dw = oracle.rmsnorm_bwd(x, w, dy, EPS32)
+
+    def loss(xx, ww):
+        xx = xx.astype(np.float64)
+        r = 1 / np.sqrt((xx ** 2).mean(-1, keepdims=True) + EPS32)
+        return float(((xx * r) * ww * dy).sum())
+
+    h = 1e-6
+    num_dx = np.zeros_like(x, np.float64)
+    for i in np.ndindex(x.shape):
+        a, b = x.astype(np.float64).copy(), x.astype(np.float64).copy()
+        a[i] += h
+        b[i] -= h
+        num_dx[i] = (loss(a, w) - loss(b, w)) / (2 * h)
+    num_dw = np.zeros(w.shape, np.float64)
+    for j in range(w.size):
+        a, b = w.astype(np.float64).copy(), w.astype(np.float64).copy()
+        a[j] += h
+        b[j] -= h
+        num_dw[j] = (loss(x, a) - loss(x, b)) / (2 * h)
+    np.testing.assert_allclose(dx, num_dx, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(dw, num_dw, rtol=1e-5, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# SwiGLU
+# --------------------------------------------------------------------------
+
+def _swiglu_inputs(shape, dtype=np.float16, seed=42):
+    r = rng(seed)
+    u = r.standard_normal(shape).astype(dtype)
+    dy = r.standard_normal((*shape[:-1], shape[-1] // 2)).astype(dtype)
+    return u, dy
+
+
+@pytest.mark.parametrize("shape", [(3, 7, 66), (64, 2048), (5, 16)])
+def test_swiglu_forward_matches_torch_with_fp16_rounding(shape):
+    u, _ = _swiglu_inputs(shape)
+    o = oracle.swiglu_fwd(u)
+    width = shape[-1] // 2
+    ut = torch.from_numpy(u)
+    g, v = ut[..., :width].float(), ut[..., width:].float()
+    ref = (F.silu(g).half().float() * v).half().numpy()
+    # torch's vectorised exp may differ from libm expf by an ulp, which can
+    # flip an fp16 rounding: allow 1 fp16 ulp on a tiny fraction of elements.
+    diff = np.abs(o.astype(np.float32) - ref.astype(np.float32))
+    ulp = np.spacing(np.abs(ref.astype(np.float16))).astype(np.float32)
+    assert np.all(diff <= ulp)
+    assert (diff > 0).mean() < 2e-3
+
+
+def test_swiglu_fp16_rounding_point_is_observable():
+    # Planted mistake: skipping the fp16 rounding of silu changes results.
+    u, _ = _swiglu_inputs((256, 512))
+    o = oracle.swiglu_fwd(u).astype(np.float32)
+    ut = torch.from_numpy(u)
+    g, v = ut[:, :256].float(), ut[:, 256:].float()
+    unrounded = (F.silu(g) * v).half().float().numpy()
+    assert (o != unrounded).mean() > 1e-3
+
+
+@pytest.mark.parametrize("shape", [(3, 7, 66), (64, 2048)])
+def test_swiglu_backward_matches_fp64_autograd(shape):
+    u, dy = _swiglu_inputs(shape)
+    du = oracle.swiglu_bwd(u, dy)
+    width = shape[-1] // 2
+    ut = torch.from_numpy(u.astype(np.float64)).requires_grad_(True)
+    out = F.silu(ut[..., :width]) * ut[..., width:]
+    out.backward(torch.from_numpy(dy.astype(np.float64)))
+    # fp16 output rounding plus the two fp16 intermediate roundings
+    np.testing.assert_allclose(du.astype(np.float64), ut.grad.numpy(), rtol=3e-3, atol=3e-3)
+
+
+def test_swiglu_backward_matches_torch_fp16_eager_autograd():
+    # torch CPU eager in fp16 has the same rounding points as the reference kernel
+    u, dy = _swiglu_inputs((32, 512), seed=5)
+    du = oracle.swiglu_bwd(u, dy)
+    ut = torch.from_numpy(u).requires_grad_(True)
+    gate, value = ut.chunk(2, -1)
+    (F.silu(gate) * value).backward(torch.from_numpy(dy))
+    ref = ut.grad.numpy().astype(np.float32)
+    diff = np.abs(du.astype(np.float32) - ref)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+    assert np.all(diff <= 2 * ulp)
+    assert (diff > 0).mean() < 5e-3
+
+
+def test_swiglu_special_values():
+    g = np.array([0.0, 30.0, -30.0, -100.0, 12.0], np.float16)
+    v = np.array([1.5, 2.0, 2.0, 3.0, -1.0], np.float16)
+    u = np.concatenate([g, v])[None, :]
+    o = oracle.swiglu_fwd(u)[0].astype(np.float32)
+    assert o[0] == 0.0 and o[1] == 60.0 and abs(o[2]) < 1e-8 and o[3] == 0.0
+    dy = np.ones((1, 5), np.float16)
+    du = oracle.swiglu_bwd(u, dy)[0].astype(np.float32)
+    assert du[0] == np.float32(np.float16(1.5)) * 0.5  # sigmoid'(0)*... = 0.5 * dy*v
+    assert du[5] == 0.0                                # dv = dy * silu(0)
+    assert du[6] == 30.0
+
+
+def test_swiglu_fp32_matches_torch():
+    u, dy = _swiglu_inputs((9, 70), np.float32)
+    o = oracle.swiglu_fwd(u)
+    du = oracle.swiglu_bwd(u, dy)
+    ut = torch.from_numpy(u).double().requires_grad_(True)
+    gate, value = ut.chunk(2, -1)
+    out = F.silu(gate) * value
+    out.backward(torch.from_numpy(dy).double())
+    np.testing.assert_allclose(o, out.detach().numpy(), rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(du, ut.grad.numpy(), rtol=2e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# Residual updates: torch's eager expression, bit for bit
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("h", [0.5, 0.25, 0.3])
+@pytest.mark.parametrize("sign", [1, -1])
+@pytest.mark.parametrize("force", [torch.float16, torch.bfloat16, torch.float32])
+def test_midpoint_bitwise_vs_eager(h, sign, force):
+    g = torch.Generator().manual_seed(11)
+    n = 40_003
+    p = torch.randn(n, generator=g)
+    a = (torch.randn(n, generator=g) * 0.3).to(force)
+    m = (torch.randn(n, generator=g) * 0.3).to(force)
+    scale = 2 * h
+    ref = p + scale * (a + m) if sign > 0 else p - scale * (a + m)
+    if force == torch.bfloat16:
+        out = oracle.midpoint(p.numpy(), a.view(torch.int16).numpy().view(np.uint16),
+                              m.view(torch.int16).numpy().view(np.uint16), scale, sign, "bf16")
+    else:
+        out = oracle.midpoint(p.numpy(), a.numpy(), m.numpy(), scale, sign)
+    assert np.array_equal(out.view(np.uint32), ref.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("force", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("sign", [1, -1])
+def test_midpoint_backward_bitwise_vs_autograd(force, sign):
+    g = torch.Generator().manual_seed(12)
+    n = 10_000
+    p = torch.randn(n, generator=g).requires_grad_(True)
+    a = torch.randn(n, generator=g).to(force).requires_grad_(True)
+    m = torch.randn(n, generator=g).to(force).requires_grad_(True)
+    dout = torch.randn(n, generator=g) * 7
+    scale = 0.6
+    out = p + scale * (a + m) if sign > 0 else p - scale * (a + m)
+    out.backward(dout)
+    name = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[force]
+    da = oracle.midpoint_bwd(dout.numpy(), scale, sign, name)
+    assert np.array_equal(da, a.grad.float().numpy())
+    assert torch.equal(a.grad, m.grad) and torch.equal(p.grad, dout)
+
+
+def test_midpoint_f64_matches_eager():
+    g = torch.Generator().manual_seed(13)
+    p, a, m = (torch.randn(1001, generator=g, dtype=torch.float64) for _ in range(3))
+    out = oracle.midpoint(p.numpy(), a.numpy(), m.numpy(), 0.5, -1)
+    assert np.array_equal(out, (p - 0.5 * (a + m)).numpy())
+
+
+@pytest.mark.parametrize("sign", [1, -1])
+def test_euler_bitwise_vs_eager(sign):
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(5000, generator=g)
+    f = torch.randn(5000, generator=g).half()
+    out = oracle.euler(x.numpy(), f.numpy(), sign)
+    ref = x + f if sign > 0 else x - f
+    assert np.array_equal(out, ref.numpy())
+
+
+# --------------------------------------------------------------------------
+# Golden file (written by tests/golden/make_golden.py)
+# --------------------------------------------------------------------------
+
+def test_oracle_reproduces_golden_vectors():
+    data = np.load(GOLDEN / "kernels_golden.npz")
+    y, rstd = oracle.rmsnorm_fwd(data["rms_x"], data["rms_w"], float(data["rms_eps"]))
+    dx, dw = oracle.rmsnorm_bwd(data["rms_x"], data["rms_w"], data["rms_dy"], float(data["rms_eps"]))
+    assert np.array_equal(y, data["rms_y"]) and np.array_equal(rstd, data["rms_rstd"])
+    assert np.array_equal(dx, data["rms_dx"]) and np.array_equal(dw, data["rms_dw"])
+    assert np.array_equal(oracle.swiglu_fwd(data["sw_u"]), data["sw_o"])
+    assert np.array_equal(oracle.swiglu_bwd(data["sw_u"], data["sw_dy"]), data["sw_du"])
+    out = oracle.midpoint(data["mp_p"], data["mp_a"], data["mp_m"], float(data["mp_scale"]), 1)
+    assert np.array_equal(out, data["mp_out"])
