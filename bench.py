@@ -19,12 +19,13 @@ data last touched a full rotation earlier.
 
 Also reported, on the same line:
   roofline      the dominant kernel (SwiGLU backward): its algorithmic bytes
-                divided by its average duration from HIP events recorded
-                around each of its launches in the timed region, against the
-                8 TB/s HBM peak; ``traffic`` is the HBM bytes per launch
-                measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), if
-                recorded.
-  kernels       the same event timing for every kernel of the step.
+                divided by its average duration (HIP events around a run of
+                back-to-back launches of that kernel on its launch stream),
+                against the 8 TB/s HBM peak; ``traffic`` is the HBM bytes per
+                launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+                (profiles/traffic.json), if recorded.
+  kernels       the same per-kernel timing for every kernel of the step
+                (rms_bwd includes its small dw-reduce launch).
   train_step    configs[3]: midpoint-reversible 7-layer decoder step
                 (B=33, T=512, fp16 autocast, GradScaler, clip 1.0, AdamW)
                 through install_v3(split core, 8192-token MLP tiles, fused
@@ -58,6 +59,8 @@ SW_BWD_BYTES = ROWS * D_FF * 2 * 5
 STEP_BYTES = RMS_FWD_BYTES + RMS_BWD_BYTES + SW_FWD_BYTES + SW_BWD_BYTES
 assert STEP_BYTES == 319_413_248
 NSETS = 6  # 6 x ~243 MB > 1 GB of distinct buffers
+COPY_BYTES = 256 << 20
+COPY_CALIBRATION_LAUNCHES = 10
 
 
 def parse_args():
@@ -120,58 +123,81 @@ class KernelStep:
         self.order = ["rms_fwd", "rms_bwd", "sw_fwd", "sw_bwd"]
         self.stream = torch.cuda.current_stream(dev).cuda_stream
 
-    def run(self, i: int, events=None) -> None:
+    def run(self, i: int) -> None:
         args = self.sets[i % len(self.sets)]["args"]
         for name in self.order:
-            if events is not None:
-                start, stop = events[name].pop()
-                start.record()
             rc = self.fns[name](*args[name], self.stream)
-            if events is not None:
-                stop.record()
             if rc:
                 raise RuntimeError(f"{name} failed with status {rc}")
 
+    def run_one(self, name: str, i: int) -> None:
+        rc = self.fns[name](*self.sets[i % len(self.sets)]["args"][name], self.stream)
+        if rc:
+            raise RuntimeError(f"{name} failed with status {rc}")
+
 
 def time_kernels(dev, steps: int, warmup: int):
+    """Headline step timing plus per-kernel averages.
+
+    Per-kernel: the kernel alone, ``steps`` launches back to back over the
+    rotating buffer sets, one HIP event pair around them on the launch stream
+    (average = elapsed / launches).  Consecutive same-stream kernels on the
+    MI355X start when the previous one ends, so this average is the kernel's
+    own duration, the quantity rocprofv3 --kernel-trace reports.
+    """
     import torch
     step = KernelStep(dev, NSETS)
     for i in range(warmup):
         step.run(i)
     torch.cuda.synchronize()
-    # Timed region 1: whole steps back to back (the headline).
     t0 = time.perf_counter()
     for i in range(steps):
         step.run(i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    # Timed region 2: the same steps with HIP events around every launch.
-    events = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(steps)] for n in step.order}
-    recorded = {n: list(v) for n, v in events.items()}
-    torch.cuda.synchronize()
-    for i in range(steps):
-        step.run(i, events)
-    torch.cuda.synchronize()
-    per_kernel = {n: sum(a.elapsed_time(b) for a, b in recorded[n]) / steps for n in step.order}
-    # spot-check the outputs of the last set against a second launch (determinism)
+    per_kernel = {}
+    for name in step.order:
+        for i in range(warmup):
+            step.run_one(name, i)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            step.run_one(name, i)
+        stop.record()
+        torch.cuda.synchronize()
+        per_kernel[name] = start.elapsed_time(stop) / steps  # ms
+    # determinism spot check: relaunch the last set, compare outputs bitwise
     s = step.sets[(steps - 1) % NSETS]
-    ref_dx, ref_du = s["dx"].clone(), s["du"].clone()
     step.run(steps - 1)
     torch.cuda.synchronize()
-    if not (torch.equal(ref_dx, s["dx"]) and torch.equal(ref_du, s["du"])):
+    ref_dx, ref_du, ref_dw = s["dx"].clone(), s["du"].clone(), s["dw"].clone()
+    step.run(steps - 1)
+    torch.cuda.synchronize()
+    if not (torch.equal(ref_dx, s["dx"]) and torch.equal(ref_du, s["du"])
+            and torch.equal(ref_dw, s["dw"])):
         raise RuntimeError("kernel outputs are not run-to-run deterministic")
     return wall / steps, per_kernel
 
 
 def kernel_loop_only(dev, steps: int, warmup: int) -> None:
-    """The kernel loop alone (rocprofv3 --kernel-trace / --pmc target)."""
+    """The kernel loop alone (rocprofv3 --kernel-trace / --pmc target), preceded
+    by COPY_CALIBRATION_LAUNCHES plain device copies of COPY_BYTES each (torch's
+    copy kernel), whose FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
+    counters against a known byte count."""
     import torch
+    src = torch.ones(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(COPY_CALIBRATION_LAUNCHES):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
     step = KernelStep(dev, NSETS)
     for i in range(warmup + steps):
         step.run(i)
     torch.cuda.synchronize()
-    print(json.dumps({"kernels_only": True, "steps": steps, "warmup": warmup}), flush=True)
+    print(json.dumps({"kernels_only": True, "steps": steps, "warmup": warmup,
+                      "copy_bytes": COPY_BYTES, "copy_launches": COPY_CALIBRATION_LAUNCHES}),
+          flush=True)
 
 
 def train_step_bench(dev, steps: int, warmup: int):

@@ -23,84 +23,86 @@ namespace {
 
 using rv::wave_sum;
 
-constexpr int kFwdWaves = 4;     // waves per block, forward
-constexpr int kBwdWaves = 8;     // waves per block, backward
+// Launch shapes chosen by timing sweeps on MI355X at the configs' shapes
+// (x [14848, 256] fp32), over > 1.5 GB of rotating buffers:
+//   forward   8 blocks of 4 waves per CU, one row per wave in flight
+//   backward  256 blocks of 16 waves, ~58 rows per block
+// Loads of x / dy are plain (they are often still in the Infinity Cache
+// when RMSNorm runs inside a model step); stores of y / dx are streaming.
+#ifndef RV_RMS_FWD_BLOCKS_PER_CU
+#define RV_RMS_FWD_BLOCKS_PER_CU 8
+#endif
+#ifndef RV_RMS_FWD_RPW
+#define RV_RMS_FWD_RPW 1
+#endif
+#ifndef RV_RMS_BWD_WAVES
+#define RV_RMS_BWD_WAVES 16
+#endif
+#ifndef RV_RMS_BWD_BLOCKS
+#define RV_RMS_BWD_BLOCKS 256
+#endif
+
+
+constexpr int kFwdWaves = 4;                 // waves per block, forward
+constexpr int kBwdWaves = RV_RMS_BWD_WAVES;  // waves per block, backward
 constexpr int kMaxVec = 16;      // float4 per lane => width <= 4096
 constexpr int kMaxEpl = 64;      // scalar path: elements per lane <= 64
 
 // ---------------------------------------------------------------------------
-// Forward, width % 4 == 0, width <= 256 * VEC.
-// With ADD the row input is x + float(f) (fused residual add) and that sum is
-// also written to h.
+// Forward, width % 4 == 0, width <= 256 * VEC.  Persistent: wave w of the
+// grid handles row groups w, w + W, w + 2W, ... (W = waves in the grid; a
+// group is RPW consecutive rows) and alternates between two register tiles,
+// issuing the next group's loads before reducing the current one.  Rows past
+// the end are clamped to the last row for loading (one cached line, no
+// branch) and never stored.  With ADD the row input is x + float(f) (fused
+// residual add) and that sum is also written to h.
 // ---------------------------------------------------------------------------
 template <int VEC, int RPW, typename F, bool ADD>
-__global__ __launch_bounds__(kFwdWaves * 64)
-void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
-                 const float* __restrict__ w, float* __restrict__ h,
-                 float* __restrict__ y, float* __restrict__ rstd,
-                 int64_t rows, int width, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t base =
-      ((int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6)) * RPW;
-  if (base >= rows) return;  // wave-uniform
+struct RowTile {
+  float4 x[RPW][VEC];
+  float4 f[ADD ? RPW : 1][VEC];
+};
 
-  // w of a column >= width only meets outputs that are never stored, so it
-  // needs no masking here.
-  float4 wv[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-    const int col = (v * 64 + lane) * 4;
-    wv[v] = rv::ld_f4(w + (col < width ? col : width - 4));
-  }
-
-  // Issue every load of the RPW rows before any arithmetic.  Out-of-range
-  // rows/columns load from a clamped, valid address and are zeroed with a
-  // select, so the loads carry no branches (a branch would make the compiler
-  // wait for each row's loads before issuing the next row's).
-  float4 xv[RPW][VEC];
-  float4 fv[ADD ? RPW : 1][VEC];
+template <int VEC, int RPW, typename F, bool ADD>
+__device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD>& t, const float* __restrict__ x,
+                                         const F* __restrict__ f, int64_t row0, int64_t rows,
+                                         int width, int lane) {
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    const int64_t row = base + r;
-    const int64_t row_c = row < rows ? row : rows - 1;
+    const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       const int col = (v * 64 + lane) * 4;
       const int col_c = col < width ? col : width - 4;
-      xv[r][v] = rv::ld_f4(x + row_c * width + col_c);
-      if constexpr (ADD) fv[r][v] = rv::load4f(f + row_c * width + col_c);
+      t.x[r][v] = rv::ld_f4(x + row * width + col_c);
+      if constexpr (ADD) t.f[r][v] = rv::load4f(f + row * width + col_c);
     }
   }
-#pragma unroll
-  for (int r = 0; r < RPW; ++r)
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const bool ok = base + r < rows && (v * 64 + lane) * 4 < width;
-      xv[r][v] = rv::keep_if(xv[r][v], ok);
-      if constexpr (ADD) fv[r][v] = rv::keep_if(fv[r][v], ok);
-    }
-  if constexpr (ADD) {
-#pragma unroll
-    for (int r = 0; r < RPW; ++r)
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        xv[r][v].x = xv[r][v].x + fv[r][v].x;
-        xv[r][v].y = xv[r][v].y + fv[r][v].y;
-        xv[r][v].z = xv[r][v].z + fv[r][v].z;
-        xv[r][v].w = xv[r][v].w + fv[r][v].w;
-      }
-  }
+}
 
+template <int VEC, int RPW, typename F, bool ADD>
+__device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const float4 (&wv)[VEC],
+                                           float* __restrict__ h, float* __restrict__ y,
+                                           float* __restrict__ rstd, int64_t row0, int64_t rows,
+                                           int width, float eps, int lane) {
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    const int64_t row = base + r;
+    const int64_t row = row0 + r;
     float ss = 0.f;
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      ss = ss + xv[r][v].x * xv[r][v].x;
-      ss = ss + xv[r][v].y * xv[r][v].y;
-      ss = ss + xv[r][v].z * xv[r][v].z;
-      ss = ss + xv[r][v].w * xv[r][v].w;
+      const bool ok = (v * 64 + lane) * 4 < width;
+      if constexpr (ADD) {
+        t.x[r][v].x = t.x[r][v].x + t.f[r][v].x;
+        t.x[r][v].y = t.x[r][v].y + t.f[r][v].y;
+        t.x[r][v].z = t.x[r][v].z + t.f[r][v].z;
+        t.x[r][v].w = t.x[r][v].w + t.f[r][v].w;
+      }
+      const float4 q = rv::keep_if(t.x[r][v], ok);
+      ss = ss + q.x * q.x;
+      ss = ss + q.y * q.y;
+      ss = ss + q.z * q.z;
+      ss = ss + q.w * q.w;
     }
     ss = wave_sum(ss);
     const float rs = rsqrtf(ss / (float)width + eps);
@@ -109,18 +111,53 @@ void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
       for (int v = 0; v < VEC; ++v) {
         const int col = (v * 64 + lane) * 4;
         if (col < width) {
-          const float4 t = xv[r][v];
+          const float4 q = t.x[r][v];
           float4 o;
-          o.x = (t.x * rs) * wv[v].x;
-          o.y = (t.y * rs) * wv[v].y;
-          o.z = (t.z * rs) * wv[v].z;
-          o.w = (t.w * rs) * wv[v].w;
-          rv::st_f4(y + row * width + col, o);
-          if constexpr (ADD) rv::st_f4(h + row * width + col, t);
+          o.x = (q.x * rs) * wv[v].x;
+          o.y = (q.y * rs) * wv[v].y;
+          o.z = (q.z * rs) * wv[v].z;
+          o.w = (q.w * rs) * wv[v].w;
+          rv::st_f4s(y + row * width + col, o);
+          if constexpr (ADD) rv::st_f4s(h + row * width + col, q);
         }
       }
       if (lane == 0) rstd[row] = rs;
     }
+  }
+}
+
+template <int VEC, int RPW, typename F, bool ADD>
+__global__ __launch_bounds__(kFwdWaves * 64)
+void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
+                 const float* __restrict__ w, float* __restrict__ h,
+                 float* __restrict__ y, float* __restrict__ rstd,
+                 int64_t rows, int width, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * kFwdWaves;
+  const int64_t wave = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
+  const int64_t groups = (rows + RPW - 1) / RPW;
+  if (wave >= groups) return;  // wave-uniform
+  const int64_t iters = (groups - 1 - wave) / nwaves + 1;
+
+  // w of a column >= width only meets outputs that are never stored.
+  float4 wv[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const int col = (v * 64 + lane) * 4;
+    wv[v] = rv::ld_f4(w + (col < width ? col : width - 4));
+  }
+  const int64_t stride = nwaves * RPW;
+  int64_t row0 = wave * RPW;
+  RowTile<VEC, RPW, F, ADD> a, b;
+  rms_load(a, x, f, row0, rows, width, lane);
+  for (int64_t k = 0; k < iters; k += 2) {
+    rms_load(b, x, f, row0 + stride, rows, width, lane);
+    rms_finish(a, wv, h, y, rstd, row0, rows, width, eps, lane);
+    if (k + 1 >= iters) break;
+    row0 += stride;
+    rms_load(a, x, f, row0 + stride, rows, width, lane);
+    rms_finish(b, wv, h, y, rstd, row0, rows, width, eps, lane);
+    row0 += stride;
   }
 }
 
@@ -165,16 +202,91 @@ void rms_fwd_scalar(const float* __restrict__ x, const F* __restrict__ f,
 
 // ---------------------------------------------------------------------------
 // Backward, width % 4 == 0.  Block b owns rows [b*rpb, min((b+1)*rpb, rows)).
-// Wave k of the block handles rows start + k*2 + {0,1}, then strides by
-// 2*kBwdWaves.  Writes dx and the block's dw partial (column-major).
+// Wave k of the block handles row pairs start + 2k, start + 2k + 2*WAVES, ...
+// alternating between two register tiles (the next pair's loads are issued
+// before the current pair is reduced).  Writes dx and the block's dw partial
+// into partial[col * ld + block] (column-major, ld >= number of blocks).
 // ---------------------------------------------------------------------------
+template <int VEC>
+struct BwdTile {
+  float4 x[2][VEC], g[2][VEC];
+  float rs[2];
+};
+
+template <int VEC>
+__device__ __forceinline__ void bwd_load(BwdTile<VEC>& t, const float* __restrict__ x,
+                                         const float* __restrict__ dy,
+                                         const float* __restrict__ rstd, int64_t row0,
+                                         int64_t end, int width, int lane) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int64_t row = row0 + r < end ? row0 + r : end - 1;  // clamped, valid
+    t.rs[r] = rstd[row];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int col = (v * 64 + lane) * 4;
+      const int col_c = col < width ? col : width - 4;
+      t.x[r][v] = rv::ld_f4(x + row * width + col_c);
+      t.g[r][v] = rv::ld_f4(dy + row * width + col_c);
+    }
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void bwd_finish(BwdTile<VEC>& t, const float4 (&wv)[VEC],
+                                           float4 (&acc)[VEC], float* __restrict__ dx,
+                                           int64_t row0, int64_t end, int width, int lane) {
+  const float fwidth = (float)width;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int64_t row = row0 + r;
+    const bool row_ok = row < end;
+    const float rs = rv::keep_if(t.rs[r], row_ok);
+    float dot = 0.f;
+    float4 g[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const bool ok = row_ok && (v * 64 + lane) * 4 < width;
+      t.x[r][v] = rv::keep_if(t.x[r][v], ok);
+      t.g[r][v] = rv::keep_if(t.g[r][v], ok);
+      g[v].x = t.g[r][v].x * wv[v].x;
+      g[v].y = t.g[r][v].y * wv[v].y;
+      g[v].z = t.g[r][v].z * wv[v].z;
+      g[v].w = t.g[r][v].w * wv[v].w;
+      dot = dot + g[v].x * t.x[r][v].x;
+      dot = dot + g[v].y * t.x[r][v].y;
+      dot = dot + g[v].z * t.x[r][v].z;
+      dot = dot + g[v].w * t.x[r][v].w;
+    }
+    dot = wave_sum(dot);
+    const float c = ((dot / fwidth) * rs) * rs;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const float4 q = t.x[r][v];
+      // dweight partial: dy * (x * r), forward multiply order.
+      acc[v].x = acc[v].x + t.g[r][v].x * (q.x * rs);
+      acc[v].y = acc[v].y + t.g[r][v].y * (q.y * rs);
+      acc[v].z = acc[v].z + t.g[r][v].z * (q.z * rs);
+      acc[v].w = acc[v].w + t.g[r][v].w * (q.w * rs);
+      const int col = (v * 64 + lane) * 4;
+      if (row_ok && col < width) {
+        float4 o;
+        o.x = (g[v].x - q.x * c) * rs;
+        o.y = (g[v].y - q.y * c) * rs;
+        o.z = (g[v].z - q.z * c) * rs;
+        o.w = (g[v].w - q.w * c) * rs;
+        rv::st_f4s(dx + row * width + col, o);
+      }
+    }
+  }
+}
+
 template <int VEC>
 __global__ __launch_bounds__(kBwdWaves * 64)
 void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
                  const float* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
-                 int64_t rows, int width, int64_t rows_per_block,
-                 int nparts) {
+                 int64_t rows, int width, int64_t rows_per_block, int ld) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t start = (int64_t)blockIdx.x * rows_per_block;
@@ -185,75 +297,25 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
     const int col = (v * 64 + lane) * 4;
-    wv[v] = rv::keep_if(rv::ld_f4(w + (col < width ? col : width - 4)),
-                        col < width);
+    wv[v] = rv::keep_if(rv::ld_f4(w + (col < width ? col : width - 4)), col < width);
     acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  const float fwidth = (float)width;
 
-  for (int64_t row0 = start + 2 * wave; row0 < end; row0 += 2 * kBwdWaves) {
-    // Branch-free loads from clamped addresses, then zero what is out of
-    // range (see rms_fwd_vec).
-    float4 xv[2][VEC], gv[2][VEC];
-    float rs[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int64_t row = row0 + r < end ? row0 + r : end - 1;
-      rs[r] = rstd[row];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const int col = (v * 64 + lane) * 4;
-        const int col_c = col < width ? col : width - 4;
-        xv[r][v] = rv::ld_f4(x + row * width + col_c);
-        gv[r][v] = rv::ld_f4(dy + row * width + col_c);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      rs[r] = rv::keep_if(rs[r], row0 + r < end);
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const bool ok = row0 + r < end && (v * 64 + lane) * 4 < width;
-        xv[r][v] = rv::keep_if(xv[r][v], ok);
-        gv[r][v] = rv::keep_if(gv[r][v], ok);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int64_t row = row0 + r;
-      float dot = 0.f;
-      float4 g[VEC];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        g[v].x = gv[r][v].x * wv[v].x;
-        g[v].y = gv[r][v].y * wv[v].y;
-        g[v].z = gv[r][v].z * wv[v].z;
-        g[v].w = gv[r][v].w * wv[v].w;
-        dot = dot + g[v].x * xv[r][v].x;
-        dot = dot + g[v].y * xv[r][v].y;
-        dot = dot + g[v].z * xv[r][v].z;
-        dot = dot + g[v].w * xv[r][v].w;
-      }
-      dot = wave_sum(dot);
-      const float c = ((dot / fwidth) * rs[r]) * rs[r];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const float4 t = xv[r][v];
-        // dweight partial: dy * (x * r), forward multiply order.
-        acc[v].x = acc[v].x + gv[r][v].x * (t.x * rs[r]);
-        acc[v].y = acc[v].y + gv[r][v].y * (t.y * rs[r]);
-        acc[v].z = acc[v].z + gv[r][v].z * (t.z * rs[r]);
-        acc[v].w = acc[v].w + gv[r][v].w * (t.w * rs[r]);
-        const int col = (v * 64 + lane) * 4;
-        if (row < end && col < width) {
-          float4 o;
-          o.x = (g[v].x - t.x * c) * rs[r];
-          o.y = (g[v].y - t.y * c) * rs[r];
-          o.z = (g[v].z - t.z * c) * rs[r];
-          o.w = (g[v].w - t.w * c) * rs[r];
-          rv::st_f4(dx + row * width + col, o);
-        }
-      }
+  const int64_t first = start + 2 * wave;
+  const int64_t stride = 2 * kBwdWaves;
+  if (first < end) {  // wave-uniform
+    const int64_t iters = (end - 1 - first) / stride + 1;
+    int64_t row0 = first;
+    BwdTile<VEC> a, b;
+    bwd_load(a, x, dy, rstd, row0, end, width, lane);
+    for (int64_t k = 0; k < iters; k += 2) {
+      bwd_load(b, x, dy, rstd, row0 + stride, end, width, lane);
+      bwd_finish(a, wv, acc, dx, row0, end, width, lane);
+      if (k + 1 >= iters) break;
+      row0 += stride;
+      bwd_load(a, x, dy, rstd, row0 + stride, end, width, lane);
+      bwd_finish(b, wv, acc, dx, row0, end, width, lane);
+      row0 += stride;
     }
   }
 
@@ -277,10 +339,10 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
       }
       const int col = (v0 * 64 + s) * 4;
       if (col < width) {
-        partial[(int64_t)(col + 0) * nparts + blockIdx.x] = t.x;
-        partial[(int64_t)(col + 1) * nparts + blockIdx.x] = t.y;
-        partial[(int64_t)(col + 2) * nparts + blockIdx.x] = t.z;
-        partial[(int64_t)(col + 3) * nparts + blockIdx.x] = t.w;
+        partial[(int64_t)(col + 0) * ld + blockIdx.x] = t.x;
+        partial[(int64_t)(col + 1) * ld + blockIdx.x] = t.y;
+        partial[(int64_t)(col + 2) * ld + blockIdx.x] = t.z;
+        partial[(int64_t)(col + 3) * ld + blockIdx.x] = t.w;
       }
     }
     __syncthreads();
@@ -297,7 +359,7 @@ void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
                     const float* __restrict__ dy, const float* __restrict__ rstd,
                     float* __restrict__ dx, float* __restrict__ partial,
                     int64_t rows, int width, int64_t rows_per_block,
-                    int nparts) {
+                    int ld) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t start = (int64_t)blockIdx.x * rows_per_block;
@@ -340,24 +402,33 @@ void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
 #pragma unroll
       for (int k = 1; k < kBwdWaves; ++k) t = t + red[k][threadIdx.x];
       const int col = j * 64 + threadIdx.x;
-      if (col < width) partial[(int64_t)col * nparts + blockIdx.x] = t;
+      if (col < width) partial[(int64_t)col * ld + blockIdx.x] = t;
     }
     __syncthreads();
   }
 }
 
-// dw[col] = sum over parts of partial[col][part]; one wavefront per column,
-// lane l sums parts l, l+64, ... in order, then a fixed-order wave sum.
+// dw[col] = sum over parts of partial[col][0:nparts] (row stride ld, a
+// multiple of 4); one wavefront per column.  Lane l sums the float4 groups
+// l, l+64, ... in order (entries >= nparts masked to zero), then a
+// fixed-order wave sum.  For nparts <= 512 every lane issues at most two
+// 16-byte loads, so the column costs one memory round trip.
 __global__ __launch_bounds__(256)
 void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
-                   int width, int nparts) {
+                   int width, int nparts, int ld) {
   const int lane = threadIdx.x & 63;
   const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (col >= width) return;
-  const float* p = partial + (int64_t)col * nparts;
+  const float* p = partial + (int64_t)col * ld;
   float s = 0.f;
-#pragma unroll 8
-  for (int i = lane; i < nparts; i += 64) s = s + p[i];
+  for (int g = lane; g * 4 < nparts; g += 64) {
+    const float4 v = rv::ld_f4(p + g * 4);
+    const int i = g * 4;
+    s = s + rv::keep_if(v.x, i + 0 < nparts);
+    s = s + rv::keep_if(v.y, i + 1 < nparts);
+    s = s + rv::keep_if(v.z, i + 2 < nparts);
+    s = s + rv::keep_if(v.w, i + 3 < nparts);
+  }
   s = wave_sum(s);
   if (lane == 0) dw[col] = s;
 }
@@ -367,14 +438,19 @@ void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
 // ---------------------------------------------------------------------------
 struct BwdPlan {
   int64_t rows_per_block;
-  int nparts;
+  int nparts;  // blocks = partial rows per column
+  int ld;      // partial column stride: nparts rounded up to a multiple of 4
 };
 
-// 512 blocks = two per compute unit on a 256-CU MI355X, all resident at
+// 256 blocks = one per compute unit on a 256-CU MI355X, all resident at
 // once, every block with the same number of rows (no partial second wave of
 // blocks).  The count is a constant, not a device query, so the dw summation
 // order -- and therefore dw bit for bit -- does not depend on the device.
-constexpr int64_t kBwdTargetBlocks = 512;
+// (Reducing the partials inside this kernel instead -- the last block to
+// finish sums them -- needs device-scope release/acquire fences, which write
+// back the per-XCD L2 on MI355X and measured 4-15x slower than this second
+// launch.)
+constexpr int64_t kBwdTargetBlocks = RV_RMS_BWD_BLOCKS;
 
 BwdPlan plan_bwd(int64_t rows) {
   const int64_t target = kBwdTargetBlocks;
@@ -383,6 +459,7 @@ BwdPlan plan_bwd(int64_t rows) {
   BwdPlan p;
   p.rows_per_block = rpb;
   p.nparts = (int)((rows + rpb - 1) / rpb);
+  p.ld = (p.nparts + 3) & ~3;
   return p;
 }
 
@@ -396,9 +473,12 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, float* y,
                    (f == nullptr ||
                     (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0);
   if (vec && width <= 256 * kMaxVec) {
-    constexpr int RPW = 2;
+    constexpr int RPW = RV_RMS_FWD_RPW;
     const int64_t rows_per_block = (int64_t)kFwdWaves * RPW;
-    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+    int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+    const int64_t cap = (int64_t)rv_host::cu_count() * RV_RMS_FWD_BLOCKS_PER_CU;
+    if (blocks > cap) blocks = cap;
+    const dim3 grid((unsigned)blocks);
     const dim3 block(kFwdWaves * 64);
     const int vecs = (width + 255) / 256;
 #define RV_FWD_VEC(V)                                                          \
@@ -469,7 +549,7 @@ int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
 int64_t rv_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
   const BwdPlan p = plan_bwd(rows);
-  return (int64_t)p.nparts * width * (int64_t)sizeof(float);
+  return (int64_t)p.ld * width * (int64_t)sizeof(float);
 }
 
 int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
@@ -480,8 +560,9 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > 4096) return RV_ERR_UNSUPPORTED;
   const BwdPlan p = plan_bwd(rows);
-  const int64_t need = (int64_t)p.nparts * width * (int64_t)sizeof(float);
+  const int64_t need = (int64_t)p.ld * width * (int64_t)sizeof(float);
   if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
+  if (!rv_host::aligned16(workspace)) return RV_ERR_WORKSPACE;
   float* partial = (float*)workspace;
   const hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)p.nparts);
@@ -494,7 +575,7 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
     const int vecs = (iw + 255) / 256;
 #define RV_BWD_VEC(V)                                                       \
   hipLaunchKernelGGL((rms_bwd_vec<V>), grid, block, 0, s, x, w, dy, rstd, dx, \
-                     partial, rows, iw, p.rows_per_block, p.nparts)
+                     partial, rows, iw, p.rows_per_block, p.ld)
     if (vecs <= 1) RV_BWD_VEC(1);
     else if (vecs <= 2) RV_BWD_VEC(2);
     else if (vecs <= 4) RV_BWD_VEC(4);
@@ -505,7 +586,7 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
     const int epl = (iw + 63) / 64;
 #define RV_BWD_SC(E)                                                          \
   hipLaunchKernelGGL((rms_bwd_scalar<E>), grid, block, 0, s, x, w, dy, rstd, dx, \
-                     partial, rows, iw, p.rows_per_block, p.nparts)
+                     partial, rows, iw, p.rows_per_block, p.ld)
     if (epl <= 1) RV_BWD_SC(1);
     else if (epl <= 2) RV_BWD_SC(2);
     else if (epl <= 4) RV_BWD_SC(4);
@@ -518,7 +599,7 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
   int st = rv_host::check_launch();
   if (st != RV_OK) return st;
   hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 3) / 4)), dim3(256),
-                     0, s, partial, dw, iw, p.nparts);
+                     0, s, partial, dw, iw, p.nparts, p.ld);
   return rv_host::check_launch();
 }
 

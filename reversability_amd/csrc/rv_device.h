@@ -62,6 +62,32 @@ __device__ __forceinline__ float round_to(float v) {
   return Conv<T>::to_f(Conv<T>::from_f(v));
 }
 
+// 16-byte global accesses, plain or streaming.  Streaming (NT = true) puts
+// the nt hint on the instruction for data touched exactly once, so a stream
+// of hundreds of MB does not evict reusable lines; each kernel picks per
+// operand what measured fastest.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  if constexpr (NT) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, uint4 v) {
+  if constexpr (NT) {
+    u32x4 t;
+    t.x = v.x; t.y = v.y; t.z = v.z; t.w = v.w;
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(p));
+  } else {
+    *reinterpret_cast<uint4*>(p) = v;
+  }
+}
+
 // 16-byte vector of T.
 template <typename T>
 struct alignas(16) Vec16 {
@@ -69,22 +95,32 @@ struct alignas(16) Vec16 {
   T v[N];
 };
 
-template <typename T>
+template <bool NT = false, typename T>
 __device__ __forceinline__ Vec16<T> load16(const T* p) {
   Vec16<T> r;
-  *reinterpret_cast<uint4*>(&r) = *reinterpret_cast<const uint4*>(p);
+  *reinterpret_cast<uint4*>(&r) = ld16<NT>(p);
   return r;
 }
-template <typename T>
+template <bool NT = false, typename T>
 __device__ __forceinline__ void store16(T* p, const Vec16<T>& r) {
-  *reinterpret_cast<uint4*>(p) = *reinterpret_cast<const uint4*>(&r);
+  st16<NT>(p, *reinterpret_cast<const uint4*>(&r));
 }
 
+// float4 access; NT = streaming.
 __device__ __forceinline__ float4 ld_f4(const float* p) {
   return *reinterpret_cast<const float4*>(p);
 }
 __device__ __forceinline__ void st_f4(float* p, float4 v) {
   *reinterpret_cast<float4*>(p) = v;
+}
+__device__ __forceinline__ float4 ld_f4s(const float* p) {
+  const uint4 u = ld16<true>(p);
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                     __uint_as_float(u.w));
+}
+__device__ __forceinline__ void st_f4s(float* p, float4 v) {
+  st16<true>(p, make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                           __float_as_uint(v.w)));
 }
 
 // Branch-free select: v if keep, else +0.0 (bit mask, so NaN/Inf inputs are

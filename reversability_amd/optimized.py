@@ -38,7 +38,8 @@ class ReusedMidpoint(torch.autograd.Function):
         p, q, *_ = ctx.saved_tensors
         grads: list = []
         scale = 2 * ctx.h
-        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype):
+        # No autocast weight-cast cache: see _InverseStack.backward.
+        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype, cache_enabled=False):
             for block in reversed(ctx.blocks):
                 with torch.enable_grad():
                     previous_q = p.detach().requires_grad_(True)

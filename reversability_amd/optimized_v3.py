@@ -156,7 +156,10 @@ class SplitMidpoint(torch.autograd.Function):
         p, q, *_ = ctx.saved_tensors
         grads: list = []
         scale = 2 * ctx.h
-        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype):
+        # No autocast weight-cast cache: the no_grad attention pass below would
+        # otherwise leave history-free fp16 weight casts for the grad-enabled
+        # rebuild (torch <= 2.10); casts are deterministic, values unchanged.
+        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype, cache_enabled=False):
             for block in reversed(ctx.blocks):
                 with torch.no_grad():
                     attention = block.attn(block.attn_norm(p))

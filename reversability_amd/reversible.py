@@ -76,7 +76,12 @@ class _InverseStack(torch.autograd.Function):
     def backward(ctx, dp, dq):
         p, q, *_ = ctx.saved_tensors
         grads: list = []
-        with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype):
+        # cache_enabled=False: torch <= 2.10 caches autocast weight casts made
+        # under no_grad (the inverse below) and hands them, without autograd
+        # history, to the grad-enabled recompute.  Casts are deterministic, so
+        # skipping the cache changes no value.
+        with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype,
+                            cache_enabled=False):
             for block in reversed(ctx.blocks):
                 with torch.no_grad():
                     p0, q0 = inverse_pair(block, p, q, ctx.method, ctx.h)

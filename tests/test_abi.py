@@ -67,5 +67,6 @@ def test_argument_validation_without_device():
 @pytest.mark.parametrize("rows,width", [(1, 8), (14848, 256), (32768, 1024), (69, 33)])
 def test_workspace_size_is_device_independent(rows, width):
     n = _hip.rmsnorm_workspace_bytes(rows, width)
-    parts = -(-rows // -(-rows // 512))
-    assert n == parts * width * 4
+    per_block = -(-rows // 256)
+    parts = -(-rows // per_block)
+    assert n == (parts + 3) // 4 * 4 * width * 4

@@ -6,11 +6,13 @@ RMSNorm (FP32): max |gpu - oracle| <= 1e-5 * max |oracle| for y, dx and dw
     (north-star bar "fp32 within max-abs 1e-5 relative to scale"); against
     torch eager F.rms_norm on the GPU the reference's own test tolerances
     (tests/test_optimized_v3.py:82-84: rtol 5e-5, atol 5e-6; dw atol 5e-5).
-SwiGLU (FP16 I/O): at most 1 fp16 ulp from the oracle on every element, on
-    under 1% of elements (the sigmoid uses the hardware exp2/rcp, whose last
-    fp32 bit can flip an fp16 rounding); against eager F.silu(g)*v the
-    reference's rtol = atol = 3e-3 (tests/test_kernels.py:49-51).  FP32 I/O:
-    2e-5.
+SwiGLU (FP16 I/O): at most 2 fp16 ulps from the oracle on every element and
+    any difference on under 1% of elements.  The sigmoid uses the hardware
+    exp2/rcp, whose last fp32 bit can flip the fp16 rounding of the
+    intermediate silu (or dy*value) by 1 ulp; the following fp16 product then
+    moves by up to 2 ulps of the output when it sits low in its binade.
+    Against eager F.silu(g)*v: the reference's rtol = atol = 3e-3
+    (tests/test_kernels.py:49-51).  FP32 I/O: 2e-5.
 Residual updates: bit-exact against the oracle and against torch's eager
     expression (same IEEE operations and rounding points).
 """
@@ -132,13 +134,13 @@ def test_add_rmsnorm_matches_oracle(cuda_device):
 SWIGLU_SHAPES = [(3, 7, 66), (14848, 2048), (4, 8192), (1, 16), (33, 1000), (2, 3, 2050)]
 
 
-def _ulp_check(actual: np.ndarray, expected: np.ndarray, max_frac=0.01):
+def _ulp_check(actual: np.ndarray, expected: np.ndarray, max_frac=0.01, max_ulp=2):
     a = actual.astype(np.float32)
     e = expected.astype(np.float32)
     diff = np.abs(a - e)
     ulp = np.spacing(np.abs(expected).astype(np.float16)).astype(np.float32)
-    assert np.all(diff <= ulp), float((diff / ulp).max())
-    assert (diff > 0).mean() <= max_frac
+    assert np.all(diff <= max_ulp * ulp), float((diff / ulp).max())
+    assert (diff > 0).mean() <= max_frac, float((diff > 0).mean())
 
 
 @pytest.mark.parametrize("shape", SWIGLU_SHAPES)
