@@ -8,9 +8,9 @@
 //
 // Backward is a single pass over x and dy: every wave computes dx for its
 // rows and accumulates dy * (x * rstd) per column in registers; the waves of
-// a block combine through LDS and the block writes one partial row of dw
-// (stored column-major, [width][nparts]).  A second small kernel sums the
-// partials of each column in a fixed order, one wavefront per column.
+// a block combine through LDS and the block writes one contiguous partial row
+// of dw ([nparts][width]).  A second small kernel sums each column's partials
+// in a fixed order.
 //
 // Arithmetic follows src/reversibility/kernels_v3.py:9-48 operation by
 // operation (sum/width + eps, x*r*w, g*x reduction, (g - x*c)*r, and the
@@ -205,7 +205,7 @@ void rms_fwd_scalar(const float* __restrict__ x, const F* __restrict__ f,
 // Wave k of the block handles row pairs start + 2k, start + 2k + 2*WAVES, ...
 // alternating between two register tiles (the next pair's loads are issued
 // before the current pair is reduced).  Writes dx and the block's dw partial
-// into partial[col * ld + block] (column-major, ld >= number of blocks).
+// as one contiguous row, partial[block * width + col].
 // ---------------------------------------------------------------------------
 template <int VEC>
 struct BwdTile {
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kBwdWaves * 64)
 void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
                  const float* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
-                 int64_t rows, int width, int64_t rows_per_block, int ld) {
+                 int64_t rows, int width, int64_t rows_per_block) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t start = (int64_t)blockIdx.x * rows_per_block;
@@ -338,12 +338,7 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
         t.w = t.w + red[k][s].w;
       }
       const int col = (v0 * 64 + s) * 4;
-      if (col < width) {
-        partial[(int64_t)(col + 0) * ld + blockIdx.x] = t.x;
-        partial[(int64_t)(col + 1) * ld + blockIdx.x] = t.y;
-        partial[(int64_t)(col + 2) * ld + blockIdx.x] = t.z;
-        partial[(int64_t)(col + 3) * ld + blockIdx.x] = t.w;
-      }
+      if (col < width) rv::st_f4(partial + (int64_t)blockIdx.x * width + col, t);
     }
     __syncthreads();
   }
@@ -358,8 +353,7 @@ __global__ __launch_bounds__(kBwdWaves * 64)
 void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
                     const float* __restrict__ dy, const float* __restrict__ rstd,
                     float* __restrict__ dx, float* __restrict__ partial,
-                    int64_t rows, int width, int64_t rows_per_block,
-                    int ld) {
+                    int64_t rows, int width, int64_t rows_per_block) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t start = (int64_t)blockIdx.x * rows_per_block;
@@ -402,35 +396,39 @@ void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
 #pragma unroll
       for (int k = 1; k < kBwdWaves; ++k) t = t + red[k][threadIdx.x];
       const int col = j * 64 + threadIdx.x;
-      if (col < width) partial[(int64_t)col * ld + blockIdx.x] = t;
+      if (col < width) partial[(int64_t)blockIdx.x * width + col] = t;
     }
     __syncthreads();
   }
 }
 
-// dw[col] = sum over parts of partial[col][0:nparts] (row stride ld, a
-// multiple of 4); one wavefront per column.  Lane l sums the float4 groups
-// l, l+64, ... in order (entries >= nparts masked to zero), then a
-// fixed-order wave sum.  For nparts <= 512 every lane issues at most two
-// 16-byte loads, so the column costs one memory round trip.
-__global__ __launch_bounds__(256)
+// dw[col] = sum over parts of partial[part][col] (row-major, one contiguous
+// row per backward block).  A block covers 64 columns (lane = column) with
+// kRedWaves waves; wave k sums parts k, k + kRedWaves, ... in order (their
+// loads are independent, so a wave issues them all before adding), then the
+// waves' sums are added in wave order through LDS.  Fixed order throughout.
+constexpr int kRedWaves = 16;
+
+__global__ __launch_bounds__(kRedWaves * 64)
 void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
-                   int width, int nparts, int ld) {
+                   int width, int nparts) {
   const int lane = threadIdx.x & 63;
-  const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (col >= width) return;
-  const float* p = partial + (int64_t)col * ld;
+  const int wave = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  const int col_c = col < width ? col : width - 1;
   float s = 0.f;
-  for (int g = lane; g * 4 < nparts; g += 64) {
-    const float4 v = rv::ld_f4(p + g * 4);
-    const int i = g * 4;
-    s = s + rv::keep_if(v.x, i + 0 < nparts);
-    s = s + rv::keep_if(v.y, i + 1 < nparts);
-    s = s + rv::keep_if(v.z, i + 2 < nparts);
-    s = s + rv::keep_if(v.w, i + 3 < nparts);
+#pragma unroll 8
+  for (int part = wave; part < nparts; part += kRedWaves)
+    s = s + partial[(int64_t)part * width + col_c];
+  __shared__ float red[kRedWaves][64];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0) {
+    float t = red[0][lane];
+#pragma unroll
+    for (int k = 1; k < kRedWaves; ++k) t = t + red[k][lane];
+    if (col < width) dw[col] = t;
   }
-  s = wave_sum(s);
-  if (lane == 0) dw[col] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -438,8 +436,7 @@ void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
 // ---------------------------------------------------------------------------
 struct BwdPlan {
   int64_t rows_per_block;
-  int nparts;  // blocks = partial rows per column
-  int ld;      // partial column stride: nparts rounded up to a multiple of 4
+  int nparts;  // backward blocks = partial rows
 };
 
 // 256 blocks = one per compute unit on a 256-CU MI355X, all resident at
@@ -459,7 +456,6 @@ BwdPlan plan_bwd(int64_t rows) {
   BwdPlan p;
   p.rows_per_block = rpb;
   p.nparts = (int)((rows + rpb - 1) / rpb);
-  p.ld = (p.nparts + 3) & ~3;
   return p;
 }
 
@@ -549,7 +545,7 @@ int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
 int64_t rv_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
   const BwdPlan p = plan_bwd(rows);
-  return (int64_t)p.ld * width * (int64_t)sizeof(float);
+  return (int64_t)p.nparts * width * (int64_t)sizeof(float);
 }
 
 int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
@@ -560,7 +556,7 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > 4096) return RV_ERR_UNSUPPORTED;
   const BwdPlan p = plan_bwd(rows);
-  const int64_t need = (int64_t)p.ld * width * (int64_t)sizeof(float);
+  const int64_t need = (int64_t)p.nparts * width * (int64_t)sizeof(float);
   if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
   if (!rv_host::aligned16(workspace)) return RV_ERR_WORKSPACE;
   float* partial = (float*)workspace;
@@ -575,7 +571,7 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
     const int vecs = (iw + 255) / 256;
 #define RV_BWD_VEC(V)                                                       \
   hipLaunchKernelGGL((rms_bwd_vec<V>), grid, block, 0, s, x, w, dy, rstd, dx, \
-                     partial, rows, iw, p.rows_per_block, p.ld)
+                     partial, rows, iw, p.rows_per_block)
     if (vecs <= 1) RV_BWD_VEC(1);
     else if (vecs <= 2) RV_BWD_VEC(2);
     else if (vecs <= 4) RV_BWD_VEC(4);
@@ -586,7 +582,7 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
     const int epl = (iw + 63) / 64;
 #define RV_BWD_SC(E)                                                          \
   hipLaunchKernelGGL((rms_bwd_scalar<E>), grid, block, 0, s, x, w, dy, rstd, dx, \
-                     partial, rows, iw, p.rows_per_block, p.ld)
+                     partial, rows, iw, p.rows_per_block)
     if (epl <= 1) RV_BWD_SC(1);
     else if (epl <= 2) RV_BWD_SC(2);
     else if (epl <= 4) RV_BWD_SC(4);
@@ -598,8 +594,8 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
   }
   int st = rv_host::check_launch();
   if (st != RV_OK) return st;
-  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 3) / 4)), dim3(256),
-                     0, s, partial, dw, iw, p.nparts, p.ld);
+  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 63) / 64)),
+                     dim3(kRedWaves * 64), 0, s, partial, dw, iw, p.nparts);
   return rv_host::check_launch();
 }
 

@@ -69,4 +69,4 @@ def test_workspace_size_is_device_independent(rows, width):
     n = _hip.rmsnorm_workspace_bytes(rows, width)
     per_block = -(-rows // 256)
     parts = -(-rows // per_block)
-    assert n == (parts + 3) // 4 * 4 * width * 4
+    assert n == parts * width * 4

@@ -303,3 +303,66 @@ def test_oracle_reproduces_golden_vectors():
     assert np.array_equal(oracle.swiglu_bwd(data["sw_u"], data["sw_dy"]), data["sw_du"])
     out = oracle.midpoint(data["mp_p"], data["mp_a"], data["mp_m"], float(data["mp_scale"]), 1)
     assert np.array_equal(out, data["mp_out"])
+
+
+# --------------------------------------------------------------------------
+# Model-level oracle (oracle/model_ref.py)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("method", ["midpoint", "euler", "baseline"])
+def test_model_oracle_matches_autograd_through_recurrence_fp64(method):
+    from oracle import model_ref
+    from reversability_amd import build_model
+    torch.manual_seed(9)
+    cfg = {"vocab_size": 53, "max_sequence_length": 16, "n_layers": 3, "n_heads": 2,
+           "d_model": 16, "d_ff": 32}
+    model = build_model({"model": cfg, "method": method}).double()
+    if method != "baseline":
+        model.backward_mode = "autograd"
+    ids = torch.randint(53, (3, 16))
+    labels = torch.randint(53, (3, 16))
+    labels[0, :3] = -100
+    loss = F.cross_entropy(model(ids).flatten(0, 1), labels.flatten(), ignore_index=-100)
+    loss.backward()
+    oloss, grads = model_ref.loss_and_grads(model.state_dict(), ids, labels, 3, 2, method,
+                                            dtype=torch.float64)
+    torch.testing.assert_close(oloss, loss.detach(), rtol=1e-12, atol=1e-12)
+    for name, p in model.named_parameters():
+        torch.testing.assert_close(grads[name], p.grad, rtol=1e-9, atol=1e-12, msg=name)
+
+
+def test_model_oracle_initial_loss_is_log_vocab():
+    # At init the head input has unit RMS (final norm, weight 1) and the tied
+    # head rows are N(0, 0.02^2): logits are ~N(0, s2), s2 = 0.02^2 * d_model,
+    # independent of the target, so E[CE] = ln V + s2 / 2 (Gaussian log-sum-exp).
+    from oracle import model_ref
+    from reversability_amd import ModelConfig, ReversibleLM
+    torch.manual_seed(1337)
+    model = ReversibleLM(ModelConfig(n_layers=2, max_sequence_length=64), "midpoint")
+    ids = torch.randint(50257, (2, 64))
+    loss, _ = model_ref.loss_and_grads(model.state_dict(), ids, torch.randint(50257, (2, 64)),
+                                       2, 8, "midpoint")
+    expected = np.log(50257) + 0.02 ** 2 * 256 / 2
+    assert abs(float(loss) - expected) < 0.05
+    assert abs(float(loss) - np.log(50257)) > 0.01  # the variance term is visible
+
+
+def test_model_oracle_midpoint_is_exactly_invertible_fp64():
+    # (p, q) -> (q, p + 2h f(q)) has the algebraic inverse (q - 2h f(p), p)
+    from oracle import model_ref
+    from reversability_amd import build_model
+    torch.manual_seed(4)
+    cfg = {"vocab_size": 31, "max_sequence_length": 8, "n_layers": 3, "n_heads": 2,
+           "d_model": 16, "d_ff": 32}
+    params = {k: v.double() for k, v in build_model({"model": cfg, "method": "midpoint"}).state_dict().items()}
+    x = torch.randn(2, 8, 16, dtype=torch.float64)
+    states = []
+    model_ref.core(params, x, 3, 2, "midpoint", 0.5, record=states)
+    p, q = states[-1]
+    for i in range(2, -1, -1):
+        a = model_ref._A(params, i, p, 2)
+        force = a + model_ref._M(params, i, p + a)
+        p, q = q - 1.0 * force, p
+        # q is the previous step's reconstructed p: exact up to rounding
+        torch.testing.assert_close(p, states[i][0], rtol=0, atol=1e-13)
+        torch.testing.assert_close(q, states[i][1], rtol=0, atol=1e-13)
