@@ -1,0 +1,285 @@
+"""Model-level GPU parity: reconstruction gate, tiled MLP block and
+the full midpoint-reversible training step.
+
+Bars (north star / the reference's own gates)
+--------------------------------------------
+* reconstruction and gradient gate: scripts/validate_reversible.py:20-29
+  tolerance tables (fp16: atol 5e-3, rtol 5e-2; fp32: atol 3e-5, rtol 3e-4;
+  fp64: atol 1e-9, rtol 1e-8; update relative L2 0.05 / 0.01 / 1e-7);
+* fp16-autocast outputs and gradients: relative L2 <= 2e-2 against the eager
+  autograd path on the GPU and against the fp32 CPU oracle;
+* tiled MLP boundary: scripts/benchmark_midpoint_v3.py:44-45 limits over two
+  AdamW updates.
+"""
+from __future__ import annotations
+
+import copy
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from reconstruction_gate import TOLERANCES, check_case
+from reversability_amd import build_model
+from reversability_amd.kernels_v3 import FusedRMSNorm
+from reversability_amd.optimized_v3 import TiledMLP, install_v3
+from reversability_amd.reversible import forward_pair, inverse_pair
+
+pytestmark = pytest.mark.gpu
+EPS32 = float(torch.finfo(torch.float32).eps)
+
+
+def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+# --------------------------------------------------------------------------
+# Reconstruction gate on the GPU (validate_reversible --device cuda)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("method", ["midpoint", "euler"])
+@pytest.mark.parametrize("precision", ["fp64", "fp32", "fp16"])
+def test_reconstruction_gate_plain(cuda_device, method, precision):
+    for depth, length in [(1, 8), (3, 17), (7, 32)]:
+        check_case(method, precision, cuda_device, depth, length)
+
+
+def _install_all(method):
+    def prepare(model):
+        if method == "midpoint":
+            install_v3(model, core_mode="split", mlp_tokens=13, swiglu=True, rmsnorm=True)
+        else:
+            install_v3(model, core_mode="reference", mlp_tokens=13, swiglu=True, rmsnorm=True)
+    return prepare
+
+
+@pytest.mark.parametrize("method", ["midpoint", "euler"])
+@pytest.mark.parametrize("precision", ["fp32", "fp16"])
+def test_reconstruction_gate_fused_v3(cuda_device, method, precision):
+    check_case(method, precision, cuda_device, 3, 17, prepare=_install_all(method))
+
+
+@pytest.mark.parametrize("core", ["reuse", "split"])
+def test_reconstruction_gate_optimized_cores_fp16(cuda_device, core):
+    check_case("midpoint", "fp16", cuda_device, 3, 17,
+               prepare=lambda m: install_v3(m, core_mode=core, swiglu=True, rmsnorm=True))
+
+
+@pytest.mark.parametrize("method", ["midpoint", "euler"])
+@pytest.mark.parametrize("precision", ["fp32", "fp16"])
+def test_architecture_sized_probe(cuda_device, method, precision):
+    """validate_reversible.py:141: 7 layers x 512 tokens x width 256, 8 heads."""
+    report = check_case(method, precision, cuda_device, 7, 512, width=256, heads=8,
+                        prepare=_install_all(method))
+    worst = max(v["max_abs"] for k, v in report["errors"].items() if k.startswith("state_"))
+    # The reference recorded (T4, fp16 AMP) worst state errors of 7.63e-5
+    # (midpoint) and 9.54e-5 (Euler); the gate itself is atol 5e-3.
+    print(f"\n[probe] {method} {precision} worst reconstructed-state max-abs {worst:.3e}", flush=True)
+    assert worst < TOLERANCES[precision]["atol"]
+
+
+# --------------------------------------------------------------------------
+# tiled SwiGLU MLP block under fp16 autocast, fp32 residual
+# --------------------------------------------------------------------------
+
+def _mlp_block_inputs(device, rows_shape=(29, 512)):
+    g = torch.Generator().manual_seed(1337)
+    d, f = 256, 1024
+    x = torch.randn(*rows_shape, d, generator=g)
+    w_up = 0.02 * torch.randn(2 * f, d, generator=g)
+    w_down = 0.02 / math.sqrt(2 * 7) * torch.randn(d, f, generator=g)
+    upstream = torch.randn(*rows_shape, d, generator=g)
+    norm_w = torch.ones(d)
+    return [t.to(device) for t in (x, norm_w, w_up, w_down, upstream)]
+
+
+def _block_candidate(x, norm_w, w_up, w_down, tokens):
+    with torch.autocast("cuda", dtype=torch.float16):
+        h = FusedRMSNorm.apply(x, norm_w, EPS32)
+        return TiledMLP.apply(h, w_up, w_down, tokens, True)
+
+
+def _block_eager(x, norm_w, w_up, w_down):
+    with torch.autocast("cuda", dtype=torch.float16):
+        h = F.rms_norm(x, (x.shape[-1],), norm_w, eps=EPS32)
+        gate, value = F.linear(h, w_up).chunk(2, -1)
+        return F.linear(F.silu(gate) * value, w_down)
+
+
+def test_tiled_mlp_block_matches_eager_and_oracle(cuda_device):
+    from oracle import model_ref
+    x, norm_w, w_up, w_down, upstream = _mlp_block_inputs(cuda_device)
+    leaves = [t.clone().requires_grad_(True) for t in (x, norm_w, w_up, w_down)]
+    ref_leaves = [t.clone().requires_grad_(True) for t in (x, norm_w, w_up, w_down)]
+    y = _block_candidate(*leaves, 8192)
+    ref = _block_eager(*ref_leaves)
+    assert y.dtype == ref.dtype == torch.float16
+    (y.float() * upstream).sum().backward()
+    (ref.float() * upstream).sum().backward()
+    assert rel_l2(y, ref) < 2e-3
+    for a, b, name in zip(leaves, ref_leaves, ["x", "norm_w", "w_up", "w_down"]):
+        assert rel_l2(a.grad, b.grad) < 2e-2, name
+    # fp32 CPU oracle on the first 2 sequences (the candidate on the same rows)
+    sub = [t[:2].detach().cpu() for t in (x, upstream)]
+    cpu = [sub[0].clone().requires_grad_(True)] + [t.detach().cpu().clone().requires_grad_(True)
+                                                  for t in (norm_w, w_up, w_down)]
+    oy = model_ref.mlp(model_ref.rms_norm(cpu[0], cpu[1]), cpu[2], cpu[3])
+    (oy * sub[1]).sum().backward()
+    part = [t[:2].clone().requires_grad_(True) if i == 0 else t.clone().requires_grad_(True)
+            for i, t in enumerate((x, norm_w, w_up, w_down))]
+    py = _block_candidate(*part, 8192)
+    (py.float() * upstream[:2]).sum().backward()
+    assert rel_l2(py.float(), oy) < 2e-2
+    for a, b, name in zip(part, cpu, ["x", "norm_w", "w_up", "w_down"]):
+        assert rel_l2(a.grad, b.grad) < 2e-2, name
+
+
+def test_tiled_mlp_boundary_gate(cuda_device):
+    """benchmark_midpoint_v3.tile_gate: configured tile + a 17-row tail vs the
+    untiled MLP module, two AdamW updates (fp16 autocast limits)."""
+    torch.manual_seed(1337)
+    model = build_model({"model": {"vocab_size": 101, "n_layers": 7}, "method": "midpoint"})
+    left = copy.deepcopy(model.blocks[0].mlp).to(cuda_device)
+    right = copy.deepcopy(left)
+    del model
+    opt_kw = dict(lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    a = torch.optim.AdamW(left.parameters(), **opt_kw)
+    b = torch.optim.AdamW(right.parameters(), **opt_kw)
+    limits = {"gradient_relative_l2": .02, "loss_relative": .002,
+              "optimizer_step_max_absolute": .0012, "optimizer_relative_update_l2": .05}
+    tokens, scale = 8192, 128.0
+    rows = tokens + 17
+    for _ in range(2):
+        a.zero_grad(set_to_none=True)
+        b.zero_grad(set_to_none=True)
+        x = torch.randn(rows, 256, device=cuda_device, requires_grad=True)
+        y = x.detach().clone().requires_grad_(True)
+        upstream = torch.randn_like(x)
+        with torch.autocast("cuda", dtype=torch.float16):
+            out = left(x)
+            cand = TiledMLP.apply(y, right.up.weight, right.down.weight, tokens, True)
+            loss = (out.float() * upstream).sum() / rows
+            other = (cand.float() * upstream).sum() / rows
+        (loss * scale).backward()
+        (other * scale).backward()
+        pairs = [(x.grad / scale, y.grad / scale)]
+        for p, q in zip(left.parameters(), right.parameters()):
+            p.grad.div_(scale)
+            q.grad.div_(scale)
+            pairs.append((p.grad, q.grad))
+        grad = max(rel_l2(v, u) for u, v in pairs)
+        torch.nn.utils.clip_grad_norm_(left.parameters(), 1.0)
+        torch.nn.utils.clip_grad_norm_(right.parameters(), 1.0)
+        old = [p.detach().clone() for p in left.parameters()]
+        old_r = [p.detach().clone() for p in right.parameters()]
+        a.step()
+        b.step()
+        diff = sum((p - q).detach().double().square().sum().item()
+                   for p, q in zip(left.parameters(), right.parameters()))
+        inc = sum((p.detach() - u).double().square().sum().item()
+                  for p, u in zip(left.parameters(), old))
+        row = {"gradient_relative_l2": grad,
+               "loss_relative": float((loss - other).abs() / loss.abs().clamp_min(1e-12)),
+               "optimizer_step_max_absolute": max(
+                   float(((p.detach() - u) - (q.detach() - v)).abs().max())
+                   for p, q, u, v in zip(left.parameters(), right.parameters(), old, old_r)),
+               "optimizer_relative_update_l2": math.sqrt(diff / max(inc, 1e-30))}
+        for key, value in limits.items():
+            assert row[key] <= value, (key, row)
+
+
+# --------------------------------------------------------------------------
+# full midpoint-reversible step, B=33, T=512, fp16 autocast
+# --------------------------------------------------------------------------
+
+C4 = {"model": {"vocab_size": 50257, "max_sequence_length": 512, "n_layers": 7, "n_heads": 8,
+                "d_model": 256, "d_ff": 1024}, "method": "midpoint", "step_size": 0.5}
+
+
+def _c4_batch(device, batch=33, length=512):
+    stream = np.random.default_rng(1337).integers(0, 50257, batch * length + 1).astype(np.uint16)
+    x = torch.from_numpy(stream[:-1].astype(np.int64).reshape(batch, length)).to(device)
+    y = torch.from_numpy(stream[1:].astype(np.int64).reshape(batch, length)).to(device)
+    return x, y
+
+
+def _step_grads(model, x, y):
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 10)
+    model.zero_grad(set_to_none=True)
+    with torch.autocast("cuda", dtype=torch.float16):
+        loss = F.cross_entropy(model(x).flatten(0, 1), y.flatten(), reduction="sum") / y.numel()
+    scaler.scale(loss).backward()
+    inv = 1.0 / scaler.get_scale()
+    return loss.detach(), {n: p.grad.detach() * inv for n, p in model.named_parameters()}
+
+
+@pytest.mark.parametrize("core", ["split", "reuse", "reference"])
+def test_full_midpoint_step_matches_autograd(cuda_device, core):
+    torch.manual_seed(1337)
+    reference = build_model(C4).to(cuda_device)
+    candidate = copy.deepcopy(reference)
+    reference.backward_mode = "autograd"
+    install_v3(candidate, core_mode=core, mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    x, y = _c4_batch(cuda_device)
+    loss_r, grads_r = _step_grads(reference, x, y)
+    loss_c, grads_c = _step_grads(candidate, x, y)
+    print(f"\n[c4] core={core} loss candidate {loss_c.item():.6f} eager {loss_r.item():.6f}",
+          flush=True)
+    assert abs(loss_c.item() - loss_r.item()) <= 2e-3 * abs(loss_r.item())
+    worst = 0.0
+    for name, g in grads_r.items():
+        r = rel_l2(grads_c[name], g)
+        worst = max(worst, r)
+        assert r < 2e-2, (name, r)
+    print(f"[c4] worst parameter-gradient relative L2 {worst:.3e}", flush=True)
+    # one AdamW update (fp16 gate: update relative L2 <= 0.05)
+    before = {n: p.detach().clone() for n, p in reference.named_parameters()}
+    for model, grads in ((reference, grads_r), (candidate, grads_c)):
+        for n, p in model.named_parameters():
+            p.grad = grads[n].clone()
+        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(.9, .95), weight_decay=.1).step()
+    diff = sum((a.detach() - b.detach()).double().square().sum().item()
+               for a, b in zip(candidate.parameters(), reference.parameters()))
+    inc = sum((p.detach() - before[n]).double().square().sum().item()
+              for n, p in reference.named_parameters())
+    assert math.sqrt(diff / inc) <= 0.05
+
+
+def test_full_step_reconstruction_error(cuda_device):
+    torch.manual_seed(1337)
+    model = build_model(C4).to(cuda_device)
+    install_v3(model, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    x, _ = _c4_batch(cuda_device)
+    with torch.autocast("cuda", dtype=torch.float16), torch.no_grad():
+        p = q = model.embed(x)
+        states = [(p, q)]
+        for block in model.blocks:
+            p, q = forward_pair(block, p, q, "midpoint", 0.5)
+            states.append((p, q))
+        worst = 0.0
+        for i in range(6, -1, -1):
+            p, q = inverse_pair(model.blocks[i], p, q, "midpoint", 0.5)
+            worst = max(worst, float((p - states[i][0]).abs().max()),
+                        float((q - states[i][1]).abs().max()))
+    print(f"\n[c4] worst reconstructed-state max-abs {worst:.3e} (reference T4: 7.63e-5)", flush=True)
+    assert worst < 5e-3
+
+
+def test_full_step_matches_cpu_oracle(cuda_device):
+    """Same weights and the first two sequences: the HIP path under fp16
+    autocast against the fp32 CPU oracle (autograd through the recurrence)."""
+    from oracle import model_ref
+    torch.manual_seed(1337)
+    model = build_model(C4).to(cuda_device)
+    install_v3(model, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    x, y = _c4_batch(cuda_device, batch=2)
+    loss_c, grads_c = _step_grads(model, x, y)
+    loss_o, grads_o = model_ref.loss_and_grads(model.state_dict(), x, y, 7, 8, "midpoint")
+    print(f"\n[c4-oracle] loss candidate {loss_c.item():.6f} oracle {loss_o.item():.6f}", flush=True)
+    assert abs(loss_c.item() - loss_o.item()) <= 2e-2 * abs(loss_o.item())
+    for name, g in grads_o.items():
+        assert rel_l2(grads_c[name], g) < 2e-2, name
