@@ -166,7 +166,7 @@ def time_kernels(dev, steps: int, warmup: int):
     wall = time.perf_counter() - t0
     per_kernel = {}
     for name in step.order:
-        for i in range(warmup):
+        for i in range(max(warmup, 100)):  # let clocks settle on the short kernels
             step.run_one(name, i)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
