@@ -1,0 +1,85 @@
+"""MFMA MLP projections with fused SwiGLU epilogues (the HIP path of TiledMLP).
+
+Thin launchers over the C ABI (``rv_mlp_*`` in include/reversibility_hip.h) for
+one token tile of the SwiGLU MLP under fp16 autocast:
+
+    up_swiglu(x, W_up)          o = fp16(silu(fp16 u_g)) * fp16 u_v, u = x16 W_up16^T
+    down(o, W_down, out)        out = fp16(o W_down16^T)
+    dgate(dy, W_down, u)        du = swiglu_bwd(u, fp16(dy W_down16))
+    dx(du, W_up, out)           out = fp32(fp16(du W_up16))
+    wgrad(dy, o, du, x, ...)    dW_down (+)= fp32(fp16(dy^T o)), dW_up (+)= fp32(fp16(du^T x16))
+
+fp32 operands (weights, normalized activations) are cast to fp16 inside the
+kernels' loads -- autocast's cast, without a separate kernel.  Outputs are
+written into caller-provided slices where the tiled caller owns the buffer.
+``supported`` says whether a shape is covered (model width and hidden width
+multiples of 128); the caller uses torch's GEMMs otherwise.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._hip import RV_F16, RV_F32, _check, _stream, library
+
+
+def supported(x: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> bool:
+    d, f = x.shape[-1], down.shape[1]
+    return (x.is_cuda and x.dtype in (torch.float32, torch.float16)
+            and up.dtype == torch.float32 and down.dtype == torch.float32
+            and up.is_contiguous() and down.is_contiguous()
+            and tuple(up.shape) == (2 * f, d) and tuple(down.shape) == (d, f)
+            and d % 128 == 0 and f % 128 == 0)
+
+
+def _xcode(x):
+    return RV_F32 if x.dtype == torch.float32 else RV_F16
+
+
+def up_swiglu(x: torch.Tensor, up: torch.Tensor, keep_u: bool = False):
+    """x [rows, d] fp32/fp16 (contiguous rows), up [2f, d] fp32 -> (o, u or None)."""
+    rows, d = x.shape
+    f = up.shape[0] // 2
+    o = torch.empty(rows, f, device=x.device, dtype=torch.float16)
+    u = torch.empty(rows, 2 * f, device=x.device, dtype=torch.float16) if keep_u else None
+    _check(library().rv_mlp_up_swiglu(x.data_ptr(), _xcode(x), x.stride(0), up.data_ptr(), rows, d,
+                                      f, o.data_ptr(), u.data_ptr() if keep_u else None,
+                                      _stream(x)), "rv_mlp_up_swiglu")
+    return o, u
+
+
+def down(o: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    rows, f = o.shape
+    d = w.shape[0]
+    _check(library().rv_mlp_down(o.data_ptr(), w.data_ptr(), rows, d, f, out.data_ptr(),
+                                 _stream(o)), "rv_mlp_down")
+    return out
+
+
+def dgate(dy: torch.Tensor, w_down: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    rows, d = dy.shape
+    f = w_down.shape[1]
+    du = torch.empty(rows, 2 * f, device=dy.device, dtype=torch.float16)
+    _check(library().rv_mlp_dgate(dy.data_ptr(), w_down.data_ptr(), u.data_ptr(), rows, d, f,
+                                  du.data_ptr(), _stream(dy)), "rv_mlp_dgate")
+    return du
+
+
+def dx(du: torch.Tensor, w_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    rows, two_f = du.shape
+    d = w_up.shape[1]
+    _check(library().rv_mlp_dx(du.data_ptr(), w_up.data_ptr(), rows, d, two_f // 2,
+                               out.data_ptr(), _stream(du)), "rv_mlp_dx")
+    return out
+
+
+def wgrad(dy, o, du, x, ddown, dup, accumulate: bool) -> None:
+    rows, d = dy.shape
+    f = o.shape[1]
+    lib = library()
+    nbytes = lib.rv_mlp_wgrad_workspace_bytes(rows, d, f)
+    if nbytes < 0:
+        _check(-nbytes, "rv_mlp_wgrad_workspace_bytes")
+    ws = torch.empty(nbytes // 4, device=dy.device, dtype=torch.float32)
+    _check(lib.rv_mlp_wgrad(dy.data_ptr(), o.data_ptr(), du.data_ptr(), x.data_ptr(), _xcode(x),
+                            x.stride(0), rows, d, f, ddown.data_ptr(), dup.data_ptr(),
+                            int(accumulate), ws.data_ptr(), nbytes, _stream(dy)), "rv_mlp_wgrad")

@@ -63,14 +63,14 @@ def _swiglu_backward(u, d_o, fused):
     return du
 
 
-def tile_forward(x, up, down, fused, compute_dtype, need_output=True):
-    """One tile of the MLP in ``compute_dtype``: returns (x_c, up_c, u, o, y)."""
+def tile_forward(x, up_c, down_c, fused, compute_dtype, need_output=True):
+    """One tile of the MLP in ``compute_dtype`` (weights already cast):
+    returns (x_c, u, o, y)."""
     x_c = x.to(compute_dtype)
-    up_c = up.to(compute_dtype)
     u = torch.mm(x_c, up_c.t())
     o = _swiglu_forward(u, fused)
-    y = torch.mm(o, down.to(compute_dtype).t()) if need_output else None
-    return x_c, up_c, u, o, y
+    y = torch.mm(o, down_c.t()) if need_output else None
+    return x_c, u, o, y
 
 
 def _compute_dtype(x, amp, amp_dtype):
@@ -79,11 +79,23 @@ def _compute_dtype(x, amp, amp_dtype):
     return x.dtype
 
 
+def _use_mfma(x, up, down, fused, cdt):
+    """The fused MFMA path covers fp16 compute with fp32 weights at widths that
+    are multiples of 128; other cases keep torch's GEMMs (and the fused SwiGLU
+    kernel when ``fused``)."""
+    from . import mlp
+    return fused and cdt == torch.float16 and mlp.supported(x, up, down)
+
+
 class TiledMLP(torch.autograd.Function):
     """Save only the normalized input and weights; recompute token tiles in backward.
 
     Attention still sees all sequences; each optimizer update consumes one whole
     physical batch.  Parameter gradients return through autograd inputs.
+
+    On ROCm tensors under fp16 autocast with ``fused`` the tile's GEMMs are the
+    MFMA kernels of ``reversability_amd.mlp`` with SwiGLU (and its backward)
+    fused into the GEMM epilogues.
     """
 
     @staticmethod
@@ -97,9 +109,20 @@ class TiledMLP(torch.autograd.Function):
         cdt = _compute_dtype(x, ctx.amp, ctx.dtype)
         flat = x.reshape(-1, x.shape[-1])
         output = torch.empty((flat.shape[0], down.shape[0]), device=x.device, dtype=cdt)
-        with torch.autocast(ctx.device, enabled=False):
+        if _use_mfma(flat, up, down, fused, cdt):
+            from . import mlp
+            flat = flat.contiguous()
             for start in range(0, flat.shape[0], tokens):
-                *_, y = tile_forward(flat[start:start + tokens], up, down, fused, cdt)
+                o, _ = mlp.up_swiglu(flat[start:start + tokens], up)
+                mlp.down(o, down, output[start:start + tokens])
+            ctx.save_for_backward(x, up, down)
+            return output.reshape(*x.shape[:-1], down.shape[0])
+        with torch.autocast(ctx.device, enabled=False):
+            # autocast's F.linear casts the weights on every call; one cast per
+            # call here gives the same values
+            up_c, down_c = up.to(cdt), down.to(cdt)
+            for start in range(0, flat.shape[0], tokens):
+                *_, y = tile_forward(flat[start:start + tokens], up_c, down_c, fused, cdt)
                 output[start:start + tokens].copy_(y)
         ctx.save_for_backward(x, up, down)
         return output.reshape(*x.shape[:-1], down.shape[0])
@@ -112,21 +135,38 @@ class TiledMLP(torch.autograd.Function):
         flat = x.reshape(-1, x.shape[-1])
         dy = gradient.reshape(-1, gradient.shape[-1]).to(cdt)
         dx = torch.empty_like(flat)
-        dup = torch.zeros_like(up)
-        ddown = torch.zeros_like(down)
-        down_c = down.to(cdt)
+        if _use_mfma(flat, up, down, ctx.fused, cdt):
+            from . import mlp
+            flat, dy = flat.contiguous(), dy.contiguous()
+            dup, ddown = torch.empty_like(up), torch.empty_like(down)
+            for i, start in enumerate(range(0, flat.shape[0], ctx.tokens)):
+                stop = start + ctx.tokens
+                x_t, g = flat[start:stop], dy[start:stop]
+                o, u = mlp.up_swiglu(x_t, up, keep_u=True)
+                du = mlp.dgate(g, down, u)
+                mlp.dx(du, up, dx[start:stop])
+                mlp.wgrad(g, o, du, x_t, ddown, dup, accumulate=i > 0)
+                del o, u, du
+            return dx.reshape_as(x), dup, ddown, None, None
+        dup = ddown = None
         with torch.autocast(ctx.device, enabled=False):
+            up_c, down_c = up.to(cdt), down.to(cdt)
             for start in range(0, flat.shape[0], ctx.tokens):
                 stop = start + ctx.tokens
-                x_c, up_c, u, o, _ = tile_forward(flat[start:stop], up, down, ctx.fused, cdt,
-                                                  need_output=False)
+                x_c, u, o, _ = tile_forward(flat[start:stop], up_c, down_c, ctx.fused, cdt,
+                                            need_output=False)
                 g = dy[start:stop]
                 d_o = torch.mm(g, down_c)
-                ddown.add_(torch.mm(g.t(), o).to(down.dtype))
+                tile_ddown = torch.mm(g.t(), o).to(down.dtype)
                 du = _swiglu_backward(u, d_o, ctx.fused)
                 dx[start:stop].copy_(torch.mm(du, up_c))
-                dup.add_(torch.mm(du.t(), x_c).to(up.dtype))
-                del x_c, up_c, u, o, g, d_o, du
+                tile_dup = torch.mm(du.t(), x_c).to(up.dtype)
+                # first tile initialises the fp32 accumulators (0 + t == t)
+                ddown = tile_ddown if ddown is None else ddown.add_(tile_ddown)
+                dup = tile_dup if dup is None else dup.add_(tile_dup)
+                del x_c, u, o, g, d_o, du, tile_ddown, tile_dup
+        if dup is None:  # no rows
+            dup, ddown = torch.zeros_like(up), torch.zeros_like(down)
         return dx.reshape_as(x), dup, ddown, None, None
 
 
