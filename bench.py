@@ -210,25 +210,42 @@ def kernel_loop_only(dev, steps: int, warmup: int) -> None:
           flush=True)
 
 
-def train_step_bench(dev, steps: int, warmup: int):
-    """midpoint-reversible 7-layer step, B=33, T=512, tokens/s."""
+TRAIN_CONFIGS = {
+    # midpoint 7 layers, d 256, split core, 8192-token MLP tiles
+    "c4": {"model": {"vocab_size": 50257, "max_sequence_length": 512, "n_layers": 7,
+                     "n_heads": 8, "d_model": 256, "d_ff": 1024},
+           "method": "midpoint", "step_size": 0.5, "batch": 33, "core_mode": "split",
+           "workload": "configs[3] midpoint 7L d256 h8 ff1024 vocab50257"},
+    # Hamiltonian-Euler 12 layers, d 1024, reconstruction stack
+    "c5": {"model": {"vocab_size": 50257, "max_sequence_length": 2048, "n_layers": 12,
+                     "n_heads": 16, "d_model": 1024, "d_ff": 4096},
+           "method": "euler", "step_size": 0.5, "batch": 16, "core_mode": "reference",
+           "workload": "configs[4] euler 12L d1024 h16 ff4096 vocab50257"},
+}
+
+
+def make_train_step(dev, name: str):
+    """One full training update of a TRAIN_CONFIGS entry: fp16 autocast forward,
+    sum cross-entropy over the batch / valid targets, reconstruction backward,
+    GradScaler unscale, clip 1.0, AdamW (0.9, 0.95), wd 0.1.  Returns
+    (step function returning the summed loss, targets per step, config)."""
     import numpy as np
     import torch
     import torch.nn.functional as F
     from reversability_amd import build_model
     from reversability_amd.optimized_v3 import install_v3
 
-    batch, length = 33, 512
-    config = {"model": {"vocab_size": 50257, "max_sequence_length": 512, "n_layers": 7,
-                        "n_heads": 8, "d_model": 256, "d_ff": 1024},
-              "method": "midpoint", "step_size": 0.5}
+    cfg = TRAIN_CONFIGS[name]
+    batch, length = cfg["batch"], cfg["model"]["max_sequence_length"]
+    vocab = cfg["model"]["vocab_size"]
     torch.manual_seed(1337)
-    model = build_model(config).to(dev)
-    install_v3(model, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    model = build_model({"model": cfg["model"], "method": cfg["method"],
+                         "step_size": cfg["step_size"]}).to(dev)
+    install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True)
     opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
     scaler = torch.amp.GradScaler("cuda")
     # one uint16 stream of B*T+1 uniform ids; x = stream[:-1], y = stream[1:]
-    stream = np.random.default_rng(1337).integers(0, 50257, batch * length + 1).astype(np.uint16)
+    stream = np.random.default_rng(1337).integers(0, vocab, batch * length + 1).astype(np.uint16)
     x = torch.from_numpy(stream[:-1].astype(np.int64).reshape(batch, length)).to(dev)
     y = torch.from_numpy(stream[1:].astype(np.int64).reshape(batch, length)).to(dev)
     targets = batch * length
@@ -245,6 +262,13 @@ def train_step_bench(dev, steps: int, warmup: int):
         scaler.update()
         return loss
 
+    return step, targets, cfg
+
+
+def train_step_bench(dev, steps: int, warmup: int, name: str = "c4"):
+    """Tokens/s of one TRAIN_CONFIGS entry's full training update."""
+    import torch
+    step, targets, cfg = make_train_step(dev, name)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -255,9 +279,10 @@ def train_step_bench(dev, steps: int, warmup: int):
     dt = (time.perf_counter() - t0) / steps
     return {"tokens_per_s": targets / dt, "ms_per_step": dt * 1e3,
             "loss": float(loss.item()) / targets, "steps": steps, "warmup": warmup,
-            "config": {"workload": "configs[3] midpoint 7L d256 h8 ff1024 vocab50257",
-                       "global_batch": batch, "seq_len": length,
-                       "core_mode": "split", "mlp_tokens": 8192, "precision": "fp16-autocast"},
+            "config": {"workload": cfg["workload"], "global_batch": cfg["batch"],
+                       "seq_len": cfg["model"]["max_sequence_length"],
+                       "core_mode": cfg["core_mode"], "mlp_tokens": 8192,
+                       "precision": "fp16-autocast"},
             "data": "synthetic uniform token ids (seed 1337)"}
 
 

@@ -160,44 +160,50 @@ int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
 /* ------------------------------------------------------------------------
  * MLP projections on MFMA (v_mfma_f32_32x32x16_f16), fp16 operands with fp32
  * accumulation, for one token tile of the SwiGLU MLP under fp16 autocast.
- * Weights are the fp32 master copies (W_up [2f, d] = [gate; value] rows,
- * W_down [d, f]); fp32 operands are rounded to fp16 while loading, as
- * autocast's F.linear casts them.  d and f must be multiples of 128, rows is
- * free, row strides are multiples of 8 elements, pointers 16-byte aligned.
- * Together these replace the F.linear / FusedSwiGLU / autograd.grad calls of
- * mlp_value and TiledMLP (src/reversibility/optimized_v3.py:10-18, 29-63;
- * src/reversibility/model.py:54-56).
+ * Weights are fp16 copies of the fp32 masters (W_up [2f, d] = [gate; value]
+ * rows, W_down [d, f]) made by rv_cast_f32_f16, which is the cast autocast's
+ * F.linear applies; activations are fp16.  d and f must be multiples of 128,
+ * rows is free, row strides are multiples of 8 elements, pointers 16-byte
+ * aligned.  Together these replace the F.linear / FusedSwiGLU / autograd.grad
+ * calls of mlp_value and TiledMLP (src/reversibility/optimized_v3.py:10-18,
+ * 29-63; src/reversibility/model.py:54-56).
  */
 
-/* o[rows, f] = fp16(silu(fp16(u_g))) * fp16(u_v), u = fp16(x) W_up^T;
- * x is fp32 or fp16 (x_dtype) with row stride ldx.  If u is not NULL the
- * fp16 pre-activation u[rows, 2f] = [u_g | u_v] is written too. */
-int rv_mlp_up_swiglu(const void* x, int x_dtype, int64_t ldx, const float* w_up,
-                     int64_t rows, int64_t d, int64_t f, void* o, void* u,
-                     void* stream);
+/* dst[i] = fp16(src[i]) (round to nearest even), i < n: autocast's cast of an
+ * fp32 weight or activation for an fp16 F.linear
+ * (src/reversibility/optimized_v3.py:15-17 under torch.autocast). */
+int rv_cast_f32_f16(const float* src, void* dst, int64_t n, void* stream);
 
-/* y[rows, d] = fp16(o W_down^T), o fp16 [rows, f]. */
-int rv_mlp_down(const void* o, const float* w_down, int64_t rows, int64_t d,
+/* o[rows, f] = fp16(silu(fp16(u_g))) * fp16(u_v), u = x W_up^T; x fp16 with
+ * row stride ldx, w_up fp16 [2f, d].  If u is not NULL the fp16
+ * pre-activation u[rows, 2f] = [u_g | u_v] is written too. */
+int rv_mlp_up_swiglu(const void* x, int64_t ldx, const void* w_up, int64_t rows,
+                     int64_t d, int64_t f, void* o, void* u, void* stream);
+
+/* y[rows, d] = fp16(o W_down^T), o fp16 [rows, f], w_down fp16 [d, f]. */
+int rv_mlp_down(const void* o, const void* w_down, int64_t rows, int64_t d,
                 int64_t f, void* y, void* stream);
 
 /* du[rows, 2f] = SwiGLU backward of u at d_o = fp16(dy W_down), with the
- * rounding points of rv_swiglu_bwd; dy fp16 [rows, d], u fp16 [rows, 2f]. */
-int rv_mlp_dgate(const void* dy, const float* w_down, const void* u,
+ * rounding points of rv_swiglu_bwd; dy fp16 [rows, d], u fp16 [rows, 2f],
+ * w_down fp16 [d, f]. */
+int rv_mlp_dgate(const void* dy, const void* w_down, const void* u,
                  int64_t rows, int64_t d, int64_t f, void* du, void* stream);
 
-/* dx[rows, d] = fp32(fp16(du W_up)), du fp16 [rows, 2f]. */
-int rv_mlp_dx(const void* du, const float* w_up, int64_t rows, int64_t d,
+/* dx[rows, d] = fp32(fp16(du W_up)), du fp16 [rows, 2f], w_up fp16 [2f, d]. */
+int rv_mlp_dx(const void* du, const void* w_up, int64_t rows, int64_t d,
               int64_t f, float* dx, void* stream);
 
-/* Scratch bytes rv_mlp_wgrad needs (split-K partial sums). */
+/* Scratch bytes rv_mlp_wgrad needs (split-K partial sums; may be 0). */
 int64_t rv_mlp_wgrad_workspace_bytes(int64_t rows, int64_t d, int64_t f);
 
 /* Weight gradients of one tile, reduced over its tokens in a fixed order:
  *   ddown[d, f]  (+)= fp32(fp16(dy^T o))
- *   dup[2f, d]   (+)= fp32(fp16(du^T fp16(x)))
- * accumulate = 0 overwrites, 1 adds (the per-tile fp32 sum of TiledMLP). */
+ *   dup[2f, d]   (+)= fp32(fp16(du^T x))
+ * dy, o, du, x fp16 (x with row stride ldx); accumulate = 0 overwrites,
+ * 1 adds (the per-tile fp32 sum of TiledMLP). */
 int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x,
-                 int x_dtype, int64_t ldx, int64_t rows, int64_t d, int64_t f,
+                 int64_t ldx, int64_t rows, int64_t d, int64_t f,
                  float* ddown, float* dup, int accumulate, void* workspace,
                  int64_t workspace_bytes, void* stream);
 

@@ -48,14 +48,15 @@ SIGNATURES = {
     "rv_midpoint_update_bwd": (_I, [_P, _P, _D, _I, _I64, _I, _I, _P]),
     "rv_residual_axpy": (_I, [_P, _P, _P, _I, _I64, _I, _I, _P]),
     "rv_add_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
-    "rv_mlp_up_swiglu": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "rv_cast_f32_f16": (_I, [_P, _P, _I64, _P]),
+    "rv_mlp_up_swiglu": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "rv_mlp_down": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_dgate": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_dx": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_wgrad_workspace_bytes": (_I64, [_I64, _I64, _I64]),
-    "rv_mlp_wgrad": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _P, _I64, _P]),
+    "rv_mlp_wgrad": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I, _P, _I64, _P]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class HipExtensionError(RuntimeError):

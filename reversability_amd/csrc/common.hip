@@ -60,6 +60,6 @@ const char* rv_status_string(int status) {
 
 const char* rv_last_error(void) { return g_last_error; }
 
-int rv_abi_version(void) { return 1; }
+int rv_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -4,524 +4,810 @@
 // 10-18, 47-63) under fp16 autocast, in the canonical form
 //     C[i][j] = sum_k A(i, k) * B(j, k)      (fp16 operands, fp32 accumulate)
 //
-//   up + SwiGLU   A = x[m][d]      B = W_up[g|v][d]   -> o = fp16(silu(fp16 u_g)) * fp16 u_v
-//   down          A = o[m][f]      B = W_down[d][f]   -> y = fp16(acc)
-//   d_o + SwiGLU' A = dy[m][d]     B(f, d) = W_down[d][f] -> du = swiglu_bwd(u, fp16(acc))
-//   dx            A = du[m][j]     B(d, j) = W_up[j][d]   -> dx = fp32(fp16(acc))
-//   dW_down       A(d, m) = dy[m][d]   B(f, m) = o[m][f]   (reduce over tokens, split-K)
-//   dW_up         A(j, m) = du[m][j]   B(d, m) = x[m][d]   (reduce over tokens, split-K)
+//   up + SwiGLU   A = x16[m][d]    B = Wup16[g|v][d]    -> o = fp16(silu(fp16 u_g)) * fp16 u_v
+//   down          A = o[m][f]      B = Wdown16[d][f]    -> y = fp16(acc)
+//   d_o + SwiGLU' A = dy[m][d]     B(f, d) = Wdown16[d][f] -> du = swiglu_bwd(u, fp16(acc))
+//   dx            A = du[m][j]     B(d, j) = Wup16[j][d]   -> dx = fp32(fp16(acc))
+//   dW_down       A(d, m) = dy[m][d]   B(f, m) = o[m][f]     -> (+)= fp32(fp16(acc))
+//   dW_up         A(j, m) = du[m][j]   B(d, m) = x16[m][d]   -> (+)= fp32(fp16(acc))
 //
-// Operands are read in their stored layout: "KC" sources are k-contiguous
-// ([rows][k]); "RC" sources are [k][rows] (rows contiguous) and are transposed
-// on the way into LDS.  fp32 sources (the fp32 master weights, the fp32
-// normalized activations) are rounded to fp16 while loading, which is the
-// cast autocast's F.linear performs, so no separate cast kernels run.
+// Every operand is fp16 and is read in its stored layout.  A "KC" source is
+// [rows][k] (k contiguous) and is staged in LDS as [row][k]; fragments are one
+// ds_read_b128 per lane.  An "RC" source is [k][rows] (rows contiguous) and is
+// staged as [k][row]; fragments are two ds_read_b64_tr_b16 per lane, the
+// gfx950 LDS transpose read.  Global -> LDS copies are therefore plain 16-byte
+// row segments for both kinds, with no scatter.  The fp32 master weights and
+// the fp32 normalized activations are cast to fp16 once per call
+// (rv_cast_f32_f16) -- the cast autocast's F.linear performs.
 //
-// Tiling: a workgroup of 4 waves (2 x 2) owns a (64*TM) x 128 tile of C; each
-// wave owns TM x 2 tiles of 32 x 32 computed with v_mfma_f32_32x32x16_f16.
-// K advances 32 at a time through two LDS buffers: the next stage's global
-// loads are issued before the current stage's MFMAs, then written to the
-// other buffer; one barrier per stage.  LDS rows are padded by 8 halves
-// against bank conflicts.
+// Tiling: a workgroup of 4 waves (2 x 2) owns a BM x BN tile of C; each wave
+// owns (BM/2) x (BN/2) = TM x TN tiles of 32 x 32 computed with
+// v_mfma_f32_32x32x16_f16.  K advances 64 per stage through two LDS buffers:
+// the next stage's global loads are issued before the current stage's MFMAs
+// and written to the other buffer afterwards; one barrier per stage.
+// Tile sizes 256x256, 128x256, 128x128 and 64x128 are chosen per shape (the
+// largest one that still gives about one workgroup per CU); the choice does
+// not change any result bit, because every output element sums its k blocks
+// in the same order in every tile shape.  Weight gradients over few output
+// tiles may split the token reduction (split-K) into fp32 partials summed by a
+// second kernel in a fixed order.
 //
-// MFMA 32x32x16 lane layout (gfx950, verified on the device): lane l supplies
-// A row / B column (l % 32) and 8 k values; the 16 accumulator values of lane
-// l are C[(j/4)*8 + (l/32)*4 + j%4][l % 32], j = 0..15.  Any k order is valid
-// as long as A and B agree; here lane l carries k = (l/32)*8 + 0..7.
+// LDS layouts (bank-conflict free for the fragment reads):
+//   KC  row stride 72 halves (144 B): the 16 rows a ds_read_b128 pass touches
+//       start at 16 distinct 4-bank groups.
+//   RC  row (= k) stride chosen so that its byte size is 64 mod 256: the four
+//       k rows one 32-lane pass of ds_read_b64_tr_b16 touches fill 4 disjoint
+//       64-byte bank ranges.
+//
+// MFMA 32x32x16 lane layout (gfx950): lane l supplies A row / B row (l % 32)
+// with k = (l/32)*8 + 0..7; accumulator value j of lane l is
+// C[(j/4)*8 + (l/32)*4 + j%4][l % 32].  The kernel issues the product as
+// B * A^T, so its accumulator holds the transposed tile: lane l owns C row
+// l % 32 and four consecutive columns per group of four values.
+//
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, lane i receives
+// element (i % 4) of the 8-byte chunks addressed by lanes 4e + i/4, e = 0..3.
+// With lanes 4e..4e+3 addressing 16 consecutive halves of LDS row e, lane i
+// receives column i of rows 0..3: a 4 (k) x 16 (row) block, transposed.
 
 #include "rv_device.h"
 
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // 16-byte staging word
+#define RV_LDS __attribute__((address_space(3)))
 
 constexpr int kThreads = 256;
-constexpr int kBN = 128;        // B rows (output columns) per workgroup
-constexpr int kBK = 32;         // k per pipeline stage
-constexpr int kLds = kBK + 8;   // padded LDS row, halves (80 bytes)
+constexpr int kBK = 32;             // k per pipeline stage
+constexpr int kStages = 4;          // depth of the LDS ring
+constexpr int kCUs = 256;           // MI355X compute units (tile-shape choice only)
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, gfx9 data format
 
-// ---------------------------------------------------------------------------
-// fp32 / fp16 -> packed fp16 helpers
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  const __half2 h = __floats2half2_rn(a, b);
-  return *reinterpret_cast<const uint32_t*>(&h);
-}
-__device__ __forceinline__ uint4 pack8(const float* v) {
-  return make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+// XOR swizzles of the 16-byte chunk index inside one LDS row (see the layout
+// notes at the top of the file).
+__device__ __forceinline__ int f_kc(int row) { return ((row >> 2) & 3) ^ (row & 2); }
+template <int ROWS>
+__device__ __forceinline__ int f_rc(int k) {
+  return ((ROWS >= 128 ? 0xCA60 : 0x6420) >> ((k & 3) * 4)) & 0xF;
 }
 
-// 8 consecutive elements of a row, returned as 8 packed fp16.
-template <typename T> __device__ __forceinline__ uint4 load8(const T* p);
-template <> __device__ __forceinline__ uint4 load8<__half>(const __half* p) {
-  return *reinterpret_cast<const uint4*>(p);
+// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-template <> __device__ __forceinline__ uint4 load8<float>(const float* p) {
-  const float4 a = *reinterpret_cast<const float4*>(p);
-  const float4 b = *reinterpret_cast<const float4*>(p + 4);
-  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  return pack8(v);
+
+// Workgroup barrier that orders this wave's LDS accesses in program order
+// (compiler barriers on both sides) without the release fence of
+// __syncthreads, which would wait for every outstanding LDS DMA.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // ---------------------------------------------------------------------------
-// Tile loaders.  A loader moves one [ROWS][kBK] fp16 tile of an operand into
-// LDS (row-major, row stride kLds).  load() issues the global loads into
-// registers; store() writes them to LDS.  Rows past `rows` are clamped to a
-// valid row (their results are never stored); k past `kmax` load zeros.
+// Row maps for KC sources: LDS row r of the tile -> source row.
 // ---------------------------------------------------------------------------
-
-// Source [rows][ld], k contiguous.  A row may be remapped (gate/value gather).
-template <typename T, int ROWS>
-struct LoadKC {
-  static constexpr int kVec = ROWS * kBK / 8 / kThreads;  // 16-byte vectors per thread
-  uint4 r[kVec];
-  template <class RowMap>
-  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t ld, const RowMap& map,
-                                       int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      const int v = threadIdx.x + i * kThreads;
-      const int row = v / (kBK / 8);
-      const int kv = (v % (kBK / 8)) * 8;
-      r[i] = load8<T>(base + map(row) * ld + k0 + kv);
-    }
-  }
-  __device__ __forceinline__ void store(_Float16* lds) const {
-#pragma unroll
-    for (int i = 0; i < kVec; ++i) {
-      const int v = threadIdx.x + i * kThreads;
-      const int row = v / (kBK / 8);
-      const int kv = (v % (kBK / 8)) * 8;
-      *reinterpret_cast<uint4*>(lds + row * kLds + kv) = r[i];
-    }
-  }
-};
-
-// Source [k][ld] with the tile's rows contiguous (a transposed operand).  Each
-// thread owns 8 consecutive rows x 2 consecutive k: two row-vector loads, then
-// eight 4-byte LDS writes of (k, k+1) pairs.  k >= kmax reads as zero.
-template <typename T, int ROWS>
-struct LoadRC {
-  static constexpr int kChunks = ROWS / 8;                   // 8-row chunks per k
-  static constexpr int kPairs = kThreads / kChunks;          // k pairs covered per pass
-  static constexpr int kPass = kBK / 2 / kPairs;             // passes per stage
-  static_assert(kPass >= 1 && kChunks * kPairs == kThreads, "RC tile shape");
-  uint4 r[kPass][2];
-  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t ld, int64_t row0,
-                                       int64_t k0, int64_t kmax) {
-    const int chunk = threadIdx.x % kChunks;
-#pragma unroll
-    for (int p = 0; p < kPass; ++p) {
-      const int kk = ((threadIdx.x / kChunks) + p * kPairs) * 2;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t k = k0 + kk + h;
-        const int64_t kc = k < kmax ? k : kmax - 1;  // clamp, then zero below
-        uint4 v = load8<T>(base + kc * ld + row0 + chunk * 8);
-        if (k >= kmax) v = make_uint4(0u, 0u, 0u, 0u);
-        r[p][h] = v;
-      }
-    }
-  }
-  __device__ __forceinline__ void store(_Float16* lds) const {
-    const int chunk = threadIdx.x % kChunks;
-#pragma unroll
-    for (int p = 0; p < kPass; ++p) {
-      const int kk = ((threadIdx.x / kChunks) + p * kPairs) * 2;
-      const uint32_t* lo = reinterpret_cast<const uint32_t*>(&r[p][0]);
-      const uint32_t* hi = reinterpret_cast<const uint32_t*>(&r[p][1]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // element e of the row chunk: low/high halves of word e/2
-        const uint32_t a = (e & 1) ? (lo[e >> 1] >> 16) : (lo[e >> 1] & 0xffffu);
-        const uint32_t b = (e & 1) ? (hi[e >> 1] >> 16) : (hi[e >> 1] & 0xffffu);
-        *reinterpret_cast<uint32_t*>(lds + (chunk * 8 + e) * kLds + kk) = a | (b << 16);
-      }
-    }
-  }
-};
-
-struct RowsDirect {  // LDS row r -> source row row0 + r, clamped to [0, rows)
+struct MapDirect {  // row0 + r, clamped to the last valid row (results never stored)
   int64_t row0, rows;
   __device__ __forceinline__ int64_t operator()(int r) const {
     const int64_t g = row0 + r;
     return g < rows ? g : rows - 1;
   }
 };
-struct RowsGateValue {  // LDS rows 0..63 -> gate rows n0.., 64..127 -> value rows F + n0..
-  int64_t n0, f;
+// SwiGLU up projection: a BN-row B tile holds BN/2 output columns, as gate
+// and value halves per wave column: rows [wn*BN/2, wn*BN/2 + BN/4) are gate
+// rows col0 + wn*BN/4 + w, the next BN/4 are the value rows f + the same.
+template <int BN>
+struct MapGateValue {
+  int64_t col0, f;
   __device__ __forceinline__ int64_t operator()(int r) const {
-    return r < 64 ? n0 + r : f + n0 + (r - 64);
+    constexpr int kHalf = BN / 2, kQuarter = BN / 4;
+    const int wn = r / kHalf, w = r % kHalf;
+    return w < kQuarter ? col0 + wn * kQuarter + w : f + col0 + wn * kQuarter + (w - kQuarter);
   }
 };
 
 // ---------------------------------------------------------------------------
-// MFMA core: acc[tm][tn] += A_tile * B_tile^T over one LDS stage.
-// Wave (wm, wn): A rows wm*32*TM + tm*32 + (l%32); B rows tn*64 + wn*32 + (l%32).
+// Global -> LDS copies: direct-to-LDS buffer loads (buffer_load_dwordx4 ...
+// lds).  One wave instruction fills 1 KB of LDS, lane L's 16 bytes at byte
+// 16 L; each lane loads the source chunk whose swizzled LDS slot that is.
+// A tile of ROWS rows is ROWS * 64 bytes per stage (kBK = 32 halves per row,
+// or 32 k rows of ROWS halves), i.e. ROWS / 16 wave instructions, ROWS / 64
+// per wave.  Per-lane source offsets are fixed; each stage adds a constant.
 // ---------------------------------------------------------------------------
-template <int TM>
-__device__ __forceinline__ void mfma_stage(const _Float16* __restrict__ a_lds,
-                                           const _Float16* __restrict__ b_lds,
-                                           f32x16 (&acc)[TM][2], int wm, int wn, int lane) {
+template <bool RC, int ROWS>
+struct Dma {
+  static constexpr int kPerWave = ROWS / 64;
+  uint32_t off[kPerWave];  // byte offset of this lane's chunk at k = 0 of the kernel's range
+  uint32_t kstep;          // bytes per stage
+  __amdgpu_buffer_rsrc_t rsrc;
+
+  // KC source [rows][ld] (k contiguous), tile rows row0..; rows past `rows`
+  // are clamped (their results are never stored); map() gathers B rows.
+  template <class Map>
+  __device__ __forceinline__ void init_kc(const __half* base, int64_t bytes, int64_t ld,
+                                          const Map& map, int64_t kbeg) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<__half*>(base), 0, (int)bytes, kRsrcWord3);
+    kstep = kBK * 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int ks = 0; ks < kBK / 16; ++ks) {
-    const int k = ks * 16 + (lane / 32) * 8;
-    f16x8 a[TM], b[2];
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-      a[tm] = *reinterpret_cast<const f16x8*>(a_lds + (wm * 32 * TM + tm * 32 + lane % 32) * kLds + k);
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
-      b[tn] = *reinterpret_cast<const f16x8*>(b_lds + (tn * 64 + wn * 32 + lane % 32) * kLds + k);
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-      for (int tn = 0; tn < 2; ++tn)
-        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[tm], b[tn], acc[tm][tn], 0, 0, 0);
+    for (int it = 0; it < kPerWave; ++it) {
+      const int b = (it * 4 + wave) * 1024 + lane * 16;
+      const int row = b >> 6, chunk = ((b >> 4) & 3) ^ f_kc(row);
+      off[it] = (uint32_t)((map(row) * ld + kbeg + chunk * 8) * 2);
+    }
   }
-}
-
-// Row of accumulator element j of lane `lane` inside a 32x32 tile.
-__device__ __forceinline__ int acc_row(int j, int lane) {
-  return (j / 4) * 8 + (lane / 32) * 4 + (j % 4);
-}
-
-// ---------------------------------------------------------------------------
-// Kernel 1: activation GEMMs, C[m][n] over m-tiles of 64*TM rows and
-// n-tiles of 128 B rows; A is a KC source; B is KC (forward) or RC (backward).
-// ---------------------------------------------------------------------------
-enum class Epi { SwiGLU, StoreF16, SwiGLUBwd, StoreF32OfF16 };
-
-struct ActArgs {
-  const void* a; int64_t lda;         // A source
-  const void* b; int64_t ldb;         // B source
-  int64_t m, n, k;                    // rows of C, columns of C (F for SwiGLU), reduction
-  void* c; int64_t ldc;               // output (o, y, du, dx)
-  void* u; int64_t ldu;               // SwiGLU: optional u output; SwiGLUBwd: u input
+  // RC source [k][ld] (tile rows contiguous from row0); k rows past the
+  // resource's end read as zero (the buffer range check).
+  __device__ __forceinline__ void init_rc(const __half* base, int64_t bytes, int64_t ld,
+                                          int64_t row0, int64_t kbeg) {
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<__half*>(base), 0, (int)bytes, kRsrcWord3);
+    kstep = (uint32_t)(kBK * ld * 2);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int it = 0; it < kPerWave; ++it) {
+      const int b = (it * 4 + wave) * 1024 + lane * 16;
+      const int krow = b / (ROWS * 2), chunk = ((b % (ROWS * 2)) >> 4) ^ f_rc<ROWS>(krow);
+      off[it] = (uint32_t)(((kbeg + krow) * ld + row0 + chunk * 8) * 2);
+    }
+  }
+  // Issue wave instruction `it` of stage `st` into the tile at `lds`; with
+  // live = false the offset is beyond any buffer's range (2 GiB > the
+  // largest operand the entry points accept): no memory is read and the
+  // lanes write zeros.
+  __device__ __forceinline__ void issue_one(_Float16* lds, int st, int it, bool live) const {
+    const int wave = threadIdx.x >> 6;
+    const uint32_t voff = live ? off[it] + (uint32_t)st * kstep : 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rsrc, (RV_LDS void*)(lds + (it * 4 + wave) * 512), 16, voff, 0, 0, 0);
+  }
+  // Issue stage `st` (relative to the kernel's first k) into the tile at `lds`.
+  __device__ __forceinline__ void issue(_Float16* lds, int st) const {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int it = 0; it < kPerWave; ++it)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (RV_LDS void*)(lds + (it * 4 + wave) * 512), 16, off[it] + (uint32_t)st * kstep,
+          0, 0, 0);
+  }
 };
 
-template <int TM, typename TA, typename TB, bool B_RC, Epi EPI>
-__global__ __launch_bounds__(kThreads, 2)
-void act_gemm(ActArgs args) {
-  constexpr int BM = 64 * TM;
-  __shared__ __attribute__((aligned(16))) _Float16 lds_a[2][BM * kLds];
-  __shared__ __attribute__((aligned(16))) _Float16 lds_b[2][kBN * kLds];
+// ---------------------------------------------------------------------------
+// MFMA fragments: lane l -> tile row r0 + l%32, k = ks*16 + (l/32)*8 + 0..7.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f16x8 frag_kc(const _Float16* lds, int r0, int ks, int lane) {
+  const int row = r0 + (lane & 31);
+  const int chunk = ks * 2 + (lane >> 5);
+  return *reinterpret_cast<const f16x8*>(lds + row * kBK + ((chunk ^ f_kc(row)) << 3));
+}
+
+// ds_read_b64_tr_b16 as inline assembly: through the builtin, the compiler
+// cannot tell the read from the in-flight LDS DMA writes and drains every
+// outstanding DMA (vmcnt(0)) before each one.  Its result is therefore not
+// tracked by the compiler's LDS counter: the k-step code waits for it
+// explicitly (lds_ready) before the MFMAs that use it.
+__device__ __forceinline__ i16x4 tr_read(const _Float16* p) {
+  i16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1"
+               : "=v"(r)
+               : "v"((uint32_t)(size_t)(RV_LDS const void*)p));
+  return r;
+}
+
+template <int ROWS>
+__device__ __forceinline__ f16x8 frag_rc(const _Float16* lds, int r0, int ks, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int m = r0 + (g & 1) * 16 + 4 * (i & 3);
+  const int k = ks * 16 + (g >> 1) * 8 + (i >> 2);
+  const int k4 = k + 4;
+  const i16x4 lo = tr_read(lds + k * ROWS + ((f_rc<ROWS>(k) ^ (m >> 3)) << 3) + (m & 7));
+  const i16x4 hi = tr_read(lds + k4 * ROWS + ((f_rc<ROWS>(k4) ^ (m >> 3)) << 3) + (m & 7));
+  const f16x4 a = __builtin_bit_cast(f16x4, lo), b = __builtin_bit_cast(f16x4, hi);
+  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Wait for every LDS read of this wave, and pass a fragment through an empty
+// asm after that wait so that its users cannot be scheduled before it.
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void after_wait(f16x8& v) { asm volatile("" : "+v"(v)); }
+
+template <bool RC, int ROWS>
+__device__ __forceinline__ f16x8 frag(const _Float16* lds, int r0, int ks, int lane) {
+  if constexpr (RC) return frag_rc<ROWS>(lds, r0, ks, lane);
+  else return frag_kc(lds, r0, ks, lane);
+}
+
+// ---------------------------------------------------------------------------
+// The GEMM kernel.
+// ---------------------------------------------------------------------------
+enum class Epi {
+  SwiGLU,         // c = o fp16 [m][n/2... per MapGateValue], optional u = [u_g | u_v]
+  StoreF16,       // c fp16 = fp16(acc)
+  SwiGLUBwd,      // c = du fp16 [m][2f] from u and d_o = fp16(acc)
+  StoreF32OfF16,  // c fp32 = fp32(fp16(acc))
+  AccF32OfF16,    // c fp32 (+)= fp32(fp16(acc))
+  PartialF32,     // c fp32 partial [split][m][n] = acc
+};
+
+struct GemmArgs {
+  const __half* a; int64_t lda; int64_t a_bytes;   // source, row stride, bytes addressable
+  const __half* b; int64_t ldb; int64_t b_bytes;
+  int64_t m, n, k;         // C rows, C columns (B rows), reduction length
+  int64_t k_chunk;         // tokens per split (multiple of kBK); == k without split
+  int64_t tiles_m, tiles_n;
+  void* c; int64_t ldc;
+  void* u; int64_t ldu;    // SwiGLU: optional u output; SwiGLUBwd: u input
+  int64_t f;               // SwiGLU / SwiGLUBwd: value column offset
+  int accumulate;          // AccF32OfF16
+};
+
+// Workgroups are dispatched to the 8 XCDs round robin.  Tiles are numbered in
+// groups of 8 M-tiles (M fastest inside a group), and each XCD receives a
+// contiguous range of tile numbers, so the workgroups sharing one XCD's L2 at
+// a time cover a compact block of M x N tiles.
+__device__ __forceinline__ void tile_of(int64_t t, int64_t tiles_m, int64_t tiles_n,
+                                        int64_t& tm, int64_t& tn) {
+  const int64_t tiles = tiles_m * tiles_n;
+  if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);
+  const int64_t group = 8 * tiles_n;
+  const int64_t g = t / group, r = t % group;
+  const int64_t first = g * 8;
+  const int64_t gm = tiles_m - first < 8 ? tiles_m - first : 8;
+  tm = first + r % gm;
+  tn = r / gm;
+}
+
+template <int BM, int BN, bool A_RC, bool B_RC, Epi EPI>
+__global__ __launch_bounds__(kThreads)
+void gemm_kernel(GemmArgs args) {
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int kA = BM * kBK, kB = BN * kBK;          // halves per stage and operand
+  constexpr int kRing = kStages * (kA + kB);
+  constexpr int kStaging = 4 * (BM / 2) * (BN / 2 + 8);  // fp16 epilogue staging
+  __shared__ __attribute__((aligned(16))) _Float16 lds[kRing > kStaging ? kRing : kStaging];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // SwiGLU: a block covers 64 output columns (64 gate + 64 value B rows).
-  constexpr int kCols = (EPI == Epi::SwiGLU) ? 64 : kBN;
-  const int64_t n_blocks = args.n / kCols;
-  const int64_t mb = blockIdx.x / n_blocks;
-  const int64_t nb = blockIdx.x % n_blocks;
-  const int64_t m0 = mb * BM, n0 = nb * kCols;
+  const int64_t tiles = args.tiles_m * args.tiles_n;
+  const int64_t split = blockIdx.x / tiles;
+  int64_t tm, tn;
+  tile_of(blockIdx.x % tiles, args.tiles_m, args.tiles_n, tm, tn);
+  const int64_t m0 = tm * BM;
+  const int64_t n0 = (EPI == Epi::SwiGLU) ? tn * (BN / 2) : tn * BN;
+  const int64_t kbeg = split * args.k_chunk;
+  const int64_t kend = kbeg + args.k_chunk < args.k ? kbeg + args.k_chunk : args.k;
+  const int stages = kend > kbeg ? (int)((kend - kbeg + kBK - 1) / kBK) : 0;
 
-  const TA* A = static_cast<const TA*>(args.a);
-  const TB* B = static_cast<const TB*>(args.b);
-  LoadKC<TA, BM> la;
-  const RowsDirect amap{m0, args.m};
-  LoadKC<TB, kBN> lb_kc;
-  LoadRC<TB, kBN> lb_rc;
+  Dma<A_RC, BM> da;
+  Dma<B_RC, BN> db;
+  if constexpr (A_RC) da.init_rc(args.a, args.a_bytes, args.lda, m0, kbeg);
+  else da.init_kc(args.a, args.a_bytes, args.lda, MapDirect{m0, args.m}, kbeg);
+  if constexpr (B_RC) db.init_rc(args.b, args.b_bytes, args.ldb, n0, kbeg);
+  else if constexpr (EPI == Epi::SwiGLU)
+    db.init_kc(args.b, args.b_bytes, args.ldb, MapGateValue<BN>{n0, args.f}, kbeg);
+  else db.init_kc(args.b, args.b_bytes, args.ldb, MapDirect{n0, args.n}, kbeg);
 
-  auto issue = [&](int64_t k0) {
-    la.load(A, args.lda, amap, k0);
-    if constexpr (B_RC) {
-      lb_rc.load(B, args.ldb, n0, k0, args.k);
-    } else if constexpr (EPI == Epi::SwiGLU) {
-      lb_kc.load(B, args.ldb, RowsGateValue{n0, args.n}, k0);
-    } else {
-      lb_kc.load(B, args.ldb, RowsDirect{n0, args.n}, k0);
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Ring: stage st lives in buffer st % kStages.  The prologue issues the
+  // DMA groups of stages 0 .. kStages-2 and loads the first k step's
+  // fragments.  Iteration st then
+  //   * waits for its own DMA of stage st + 1 and joins the workgroup, so all
+  //     of stage st + 1 has landed and every wave is done with stage st - 1;
+  //   * runs stage st's two k steps of MFMAs, issuing between them -- at
+  //     fixed points (sched_barrier) -- the DMA group of stage
+  //     st + kStages - 1 into stage st - 1's buffer, the fragments of its
+  //     second k step, and the fragments of stage st + 1's first k step.
+  // A group for a stage past the end is still issued, with an offset beyond
+  // the buffer's range: it reads nothing from memory and writes zeros into a
+  // buffer no later stage uses, and every iteration waits for the same
+  // vmcnt.  Fragments prefetched past the last stage are never used.
+  constexpr int kPerWaveA = Dma<A_RC, BM>::kPerWave, kPerWave = kPerWaveA + Dma<B_RC, BN>::kPerWave;
+  constexpr int kM = TM * TN, kF = TM + TN;
+  f16x8 fa[2][TM], fb[2][TN];
+
+#define RV_FRAG(SLOT, LA, LB, KS, P)                                                        \
+  do {                                                                                      \
+    if ((P) < TM) fa[SLOT][(P)] = frag<A_RC, BM>((LA), wm * (BM / 2) + (P) * 32, (KS), lane); \
+    else fb[SLOT][(P) - TM] = frag<B_RC, BN>((LB), wn * (BN / 2) + ((P) - TM) * 32, (KS), lane); \
+  } while (0)
+#define RV_DMA(D, BUF, ST, LIVE)                                                            \
+  do {                                                                                      \
+    if ((D) < kPerWaveA) da.issue_one((BUF), (ST), (D), (LIVE));                             \
+    else db.issue_one((BUF) + kA, (ST), (D) - kPerWaveA, (LIVE));                            \
+  } while (0)
+  // MFMAs of fragment slot SLOT; after MFMA q, DMA instruction d goes where
+  // d * kM / kPerWave == q (if DO_DMA) and fragment f of (LA2, LB2, KS2) into
+  // slot SLOT ^ 1 where f * kM / kF == q.
+#define RV_KSTEP(SLOT, DO_DMA, DMABUF, DMAST, LIVE, LA2, LB2, KS2)                           \
+  do {                                                                                      \
+    if constexpr (A_RC || B_RC) {                                                           \
+      lds_wait_all();                                                                       \
+      _Pragma("unroll") for (int i_ = 0; i_ < TM; ++i_) after_wait(fa[SLOT][i_]);           \
+      _Pragma("unroll") for (int j_ = 0; j_ < TN; ++j_) after_wait(fb[SLOT][j_]);           \
+      __builtin_amdgcn_sched_barrier(0);                                                    \
+    }                                                                                       \
+    _Pragma("unroll") for (int q = 0; q < kM; ++q) {                                        \
+      acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(                          \
+          fb[SLOT][q % TN], fa[SLOT][q / TN], acc[q / TN][q % TN], 0, 0, 0);                \
+      if (DO_DMA) {                                                                         \
+        _Pragma("unroll") for (int d = 0; d < kPerWave; ++d) if (d * kM / kPerWave == q)    \
+          RV_DMA(d, (DMABUF), (DMAST), (LIVE));                                             \
+      }                                                                                     \
+      _Pragma("unroll") for (int f = 0; f < kF; ++f) if (f * kM / kF == q)                  \
+        RV_FRAG((SLOT) ^ 1, (LA2), (LB2), (KS2), f);                                        \
+      __builtin_amdgcn_sched_barrier(0);                                                    \
+    }                                                                                       \
+  } while (0)
+
+  if (stages > 0) {
+#pragma unroll
+    for (int p = 0; p < kStages - 1; ++p) {
+      _Float16* buf = lds + p * (kA + kB);
+#pragma unroll
+      for (int d = 0; d < kPerWave; ++d) RV_DMA(d, buf, p, p < stages);
     }
-  };
-  auto commit = [&](int buf) {
-    la.store(lds_a[buf]);
-    if constexpr (B_RC) lb_rc.store(lds_b[buf]); else lb_kc.store(lds_b[buf]);
-  };
-
-  f32x16 acc[TM][2];
+    wait_vmcnt<(kStages - 2) * kPerWave>();
+    lds_barrier();
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[tm][tn][j] = 0.f;
-
-  const int64_t stages = args.k / kBK;
-  issue(0);
-  commit(0);
-  __syncthreads();
-  for (int64_t s = 0; s < stages; ++s) {
-    const int buf = (int)(s & 1);
-    if (s + 1 < stages) issue((s + 1) * kBK);
-    mfma_stage<TM>(lds_a[buf], lds_b[buf], acc, wm, wn, lane);
-    if (s + 1 < stages) commit(buf ^ 1);
-    __syncthreads();
+    for (int f = 0; f < kF; ++f) RV_FRAG(0, lds, lds + kA, 0, f);
   }
+  for (int st = 0; st < stages; ++st) {
+    wait_vmcnt<(kStages - 3) * kPerWave>();
+    lds_barrier();
+    const _Float16* la = lds + (st % kStages) * (kA + kB);
+    const _Float16* ln = lds + ((st + 1) % kStages) * (kA + kB);
+    _Float16* dbuf = lds + ((st + kStages - 1) % kStages) * (kA + kB);
+    const int dst = st + kStages - 1;
+    RV_KSTEP(0, true, dbuf, dst, dst < stages, la, la + kA, 1);
+    RV_KSTEP(1, false, dbuf, dst, false, ln, ln + kA, 0);
+  }
+  wait_vmcnt<0>();  // the trailing groups' zero writes land before the ring is reused
+#undef RV_KSTEP
+#undef RV_DMA
+#undef RV_FRAG
+  __syncthreads();  // every wave is done with the ring before the epilogue reuses it
 
   // ---- epilogue ----
+  // The MFMA is issued as B * A^T, so each lane holds C row (lane % 32) of
+  // its 32x32 tile and, for q = 0..3, the 4 consecutive columns
+  // q*8 + (lane/32)*4 + 0..3 (accumulator values 4q..4q+3).
+  const int cq = (lane >> 5) * 4;
+  if constexpr (EPI == Epi::PartialF32 || EPI == Epi::StoreF32OfF16 ||
+                EPI == Epi::AccF32OfF16) {
+    // fp32 outputs: 16-byte stores straight from the accumulators.
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int64_t row = m0 + wm * 32 * TM + tm * 32 + acc_row(j, lane);
+    for (int i = 0; i < TM; ++i) {
+      const int64_t row = m0 + wm * (BM / 2) + i * 32 + (lane & 31);
       if (row >= args.m) continue;
-      if constexpr (EPI == Epi::SwiGLU) {
-        const int64_t col = n0 + wn * 32 + (lane % 32);
-        const float g = rv::round_to<__half>(acc[tm][0][j]);
-        const float v = rv::round_to<__half>(acc[tm][1][j]);
-        const float silu = rv::round_to<__half>(g * rv::fast_sigmoid(g));
-        static_cast<__half*>(args.c)[row * args.ldc + col] = __float2half_rn(silu * v);
-        if (args.u != nullptr) {
-          __half* u = static_cast<__half*>(args.u) + row * args.ldu;
-          u[col] = __float2half_rn(g);
-          u[args.n + col] = __float2half_rn(v);
-        }
-      } else {
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn) {
-          const int64_t col = n0 + tn * 64 + wn * 32 + (lane % 32);
-          const float d = rv::round_to<__half>(acc[tm][tn][j]);
-          if constexpr (EPI == Epi::StoreF16) {
-            static_cast<__half*>(args.c)[row * args.ldc + col] = __float2half_rn(d);
-          } else if constexpr (EPI == Epi::StoreF32OfF16) {
-            static_cast<float*>(args.c)[row * args.ldc + col] = d;
-          } else {  // SwiGLUBwd: du from u = [gate | value] and d_o = d
-            const __half* u = static_cast<const __half*>(args.u) + row * args.ldu;
-            const float g = __half2float(u[col]);
-            const float v = __half2float(u[args.n + col]);
-            const float s = rv::fast_sigmoid(g);
-            const float silu = rv::round_to<__half>(g * s);
-            const float dgi = rv::round_to<__half>(d * v);
-            __half* du = static_cast<__half*>(args.c) + row * args.ldc;
-            du[col] = __float2half_rn(dgi * (s * (1.0f + g * (1.0f - s))));
-            du[args.n + col] = __float2half_rn(d * silu);
+      for (int j = 0; j < TN; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t col = n0 + wn * (BN / 2) + j * 32 + q * 8 + cq;
+          const float a0 = acc[i][j][q * 4], a1 = acc[i][j][q * 4 + 1];
+          const float a2 = acc[i][j][q * 4 + 2], a3 = acc[i][j][q * 4 + 3];
+          if constexpr (EPI == Epi::PartialF32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(args.c) +
+                                       (split * args.m + row) * args.ldc + col) =
+                make_float4(a0, a1, a2, a3);
+          } else {
+            float4 r = make_float4(rv::round_to<__half>(a0), rv::round_to<__half>(a1),
+                                   rv::round_to<__half>(a2), rv::round_to<__half>(a3));
+            float4* c = reinterpret_cast<float4*>(static_cast<float*>(args.c) + row * args.ldc + col);
+            if constexpr (EPI == Epi::AccF32OfF16) {
+              if (args.accumulate) {
+                const float4 p = *c;
+                r = make_float4(p.x + r.x, p.y + r.y, p.z + r.z, p.w + r.w);
+              }
+            }
+            *c = r;
           }
         }
       }
     }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Kernel 2: weight gradients, C[i][j] = sum_m A(i, m) B(j, m) with both
-// operands RC sources ([m][i], [m][j]).  blockIdx -> (i-tile, j-tile, split);
-// split s reduces m in [s*chunk, min((s+1)*chunk, m)) and writes its fp32
-// partial tile to part[s][i][j].
-// ---------------------------------------------------------------------------
-struct WgradArgs {
-  const void* a; int64_t lda;   // [m][ni]
-  const void* b; int64_t ldb;   // [m][nj]
-  int64_t m, ni, nj, chunk;     // tokens, output rows, output cols, tokens per split
-  float* part;                  // [splits][ni][nj]
-};
-
-template <typename TA, typename TB>
-__global__ __launch_bounds__(kThreads, 2)
-void wgrad_gemm(WgradArgs args) {
-  constexpr int TM = 2, BM = 128;
-  __shared__ __attribute__((aligned(16))) _Float16 lds_a[2][BM * kLds];
-  __shared__ __attribute__((aligned(16))) _Float16 lds_b[2][kBN * kLds];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t ti = args.ni / BM, tj = args.nj / kBN;
-  const int64_t s = blockIdx.x / (ti * tj);
-  const int64_t rem = blockIdx.x % (ti * tj);
-  const int64_t i0 = (rem / tj) * BM, j0 = (rem % tj) * kBN;
-  const int64_t kbeg = s * args.chunk;
-  const int64_t kend = kbeg + args.chunk < args.m ? kbeg + args.chunk : args.m;
-
-  const TA* A = static_cast<const TA*>(args.a);
-  const TB* B = static_cast<const TB*>(args.b);
-  LoadRC<TA, BM> la;
-  LoadRC<TB, kBN> lb;
-
-  f32x16 acc[TM][2];
+  } else {
+    // fp16 outputs: each wave stages fp16(acc) for its (BM/2) x (BN/2) tile
+    // in LDS (row stride WN + 8 halves), then moves whole rows, 16 bytes per
+    // lane, so every global access instruction covers full row segments.
+    constexpr int WM = BM / 2, WN = BN / 2, S = WN + 8;
+    _Float16* stage = lds + wave * (WM * S);
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[tm][tn][j] = 0.f;
-
-  const int64_t stages = (kend - kbeg + kBK - 1) / kBK;
-  if (stages > 0) {
-    la.load(A, args.lda, i0, kbeg, kend);
-    lb.load(B, args.ldb, j0, kbeg, kend);
-    la.store(lds_a[0]);
-    lb.store(lds_b[0]);
-  }
-  __syncthreads();
-  for (int64_t st = 0; st < stages; ++st) {
-    const int buf = (int)(st & 1);
-    if (st + 1 < stages) {
-      la.load(A, args.lda, i0, kbeg + (st + 1) * kBK, kend);
-      lb.load(B, args.ldb, j0, kbeg + (st + 1) * kBK, kend);
-    }
-    mfma_stage<TM>(lds_a[buf], lds_b[buf], acc, wm, wn, lane);
-    if (st + 1 < stages) {
-      la.store(lds_a[buf ^ 1]);
-      lb.store(lds_b[buf ^ 1]);
-    }
+        for (int q = 0; q < 4; ++q) {
+          const __half2 h01 = __floats2half2_rn(acc[i][j][q * 4], acc[i][j][q * 4 + 1]);
+          const __half2 h23 = __floats2half2_rn(acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]);
+          uint2 p;
+          p.x = *reinterpret_cast<const uint32_t*>(&h01);
+          p.y = *reinterpret_cast<const uint32_t*>(&h23);
+          *reinterpret_cast<uint2*>(stage + (i * 32 + (lane & 31)) * S + j * 32 + q * 8 + cq) = p;
+        }
     __syncthreads();
-  }
-  float* out = args.part + s * args.ni * args.nj;
+    const int64_t row0 = m0 + wm * WM;
+    if constexpr (EPI == Epi::SwiGLU) {
+      // gate in staged columns [0, WN/2), value in [WN/2, WN)
+      constexpr int CPR = WN / 16, RPP = 64 / CPR;
+      const int c = lane % CPR;
+      __half* u = static_cast<__half*>(args.u);
+      const int64_t col = n0 + wn * (WN / 2) + c * 8;
+#pragma unroll 4
+      for (int r = lane / CPR; r < WM; r += RPP) {
+        const int64_t row = row0 + r;
+        if (row >= args.m) break;
+        const u32x4 gw = *reinterpret_cast<const u32x4*>(stage + r * S + c * 8);
+        const u32x4 vw = *reinterpret_cast<const u32x4*>(stage + r * S + WN / 2 + c * 8);
+        const __half* gh = reinterpret_cast<const __half*>(&gw);
+        const __half* vh = reinterpret_cast<const __half*>(&vw);
+        __half oh[8];
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int64_t row = i0 + wm * 64 + tm * 32 + acc_row(j, lane);
-        const int64_t col = j0 + tn * 64 + wn * 32 + (lane % 32);
-        out[row * args.nj + col] = acc[tm][tn][j];
+        for (int e = 0; e < 8; ++e) {
+          const float g = __half2float(gh[e]);
+          const float silu = rv::round_to<__half>(g * rv::fast_sigmoid(g));
+          oh[e] = __float2half_rn(silu * __half2float(vh[e]));
+        }
+        *reinterpret_cast<u32x4*>(static_cast<__half*>(args.c) + row * args.ldc + col) =
+            *reinterpret_cast<const u32x4*>(oh);
+        if (u != nullptr) {
+          *reinterpret_cast<u32x4*>(u + row * args.ldu + col) = gw;
+          *reinterpret_cast<u32x4*>(u + row * args.ldu + args.f + col) = vw;
+        }
       }
+    } else {
+      constexpr int CPR = WN / 8, RPP = 64 / CPR;
+      const int c = lane % CPR;
+      const int64_t col = n0 + wn * WN + c * 8;
+#pragma unroll 4
+      for (int r = lane / CPR; r < WM; r += RPP) {
+        const int64_t row = row0 + r;
+        if (row >= args.m) break;
+        const u32x4 dw = *reinterpret_cast<const u32x4*>(stage + r * S + c * 8);
+        if constexpr (EPI == Epi::StoreF16) {
+          *reinterpret_cast<u32x4*>(static_cast<__half*>(args.c) + row * args.ldc + col) = dw;
+        } else {  // SwiGLUBwd: du from u = [gate | value] and d_o = fp16(acc)
+          const __half* ur = static_cast<const __half*>(args.u) + row * args.ldu;
+          const u32x4 gw = *reinterpret_cast<const u32x4*>(ur + col);
+          const u32x4 vw = *reinterpret_cast<const u32x4*>(ur + args.f + col);
+          const __half* dh = reinterpret_cast<const __half*>(&dw);
+          const __half* gh = reinterpret_cast<const __half*>(&gw);
+          const __half* vh = reinterpret_cast<const __half*>(&vw);
+          __half dgo[8], dvo[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = __half2float(dh[e]);
+            const float g = __half2float(gh[e]);
+            const float v = __half2float(vh[e]);
+            const float sg = rv::fast_sigmoid(g);
+            const float silu = rv::round_to<__half>(g * sg);
+            const float dgi = rv::round_to<__half>(d * v);
+            dgo[e] = __float2half_rn(dgi * (sg * (1.0f + g * (1.0f - sg))));
+            dvo[e] = __float2half_rn(d * silu);
+          }
+          __half* du = static_cast<__half*>(args.c) + row * args.ldc;
+          *reinterpret_cast<u32x4*>(du + col) = *reinterpret_cast<const u32x4*>(dgo);
+          *reinterpret_cast<u32x4*>(du + args.f + col) = *reinterpret_cast<const u32x4*>(dvo);
+        }
+      }
+    }
+  }
 }
+
+// Explicit instantiations of every (tile shape, operand layout, epilogue) the
+// host dispatch can launch.  Without them this compiler emits the host-side
+// launch stubs of only some of the kernels reached through the dispatch
+// switch, and the library fails to load with undefined symbols.
+template __global__ void gemm_kernel<256, 256, false, false, Epi::SwiGLU>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, false, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::SwiGLUBwd>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, true, true, Epi::AccF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, true, true, Epi::PartialF32>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, false, Epi::SwiGLU>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, false, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, true, Epi::SwiGLUBwd>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, true, Epi::StoreF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, true, true, Epi::AccF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, true, true, Epi::PartialF32>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, false, Epi::SwiGLU>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, false, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, true, Epi::SwiGLUBwd>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, true, Epi::StoreF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, true, true, Epi::AccF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, true, true, Epi::PartialF32>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, false, Epi::SwiGLU>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, false, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, true, Epi::SwiGLUBwd>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, true, true, Epi::AccF32OfF16>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, true, true, Epi::PartialF32>(GemmArgs);
 
 // acc[i] (+)= fp32(fp16(sum_s part[s][i])), splits summed in order.  This is
 // autocast's weight gradient: the fp16 GEMM result, cast to the fp32 weight
-// and added to the running per-tile sum.
+// and added to the running per-tile sum.  n % 4 == 0.
 __global__ __launch_bounds__(256)
-void wgrad_reduce(const float* __restrict__ part, int splits, int64_t n, float* acc_out,
+void wgrad_reduce(const float* __restrict__ part, int splits, int64_t n, float* __restrict__ out,
                   int accumulate) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= n) return;
-  float s = 0.f;
-  for (int k = 0; k < splits; ++k) s = s + part[k * n + i];
-  const float g = rv::round_to<__half>(s);
-  acc_out[i] = accumulate ? acc_out[i] + g : g;
+  float4 s = *reinterpret_cast<const float4*>(part + i);
+  for (int k = 1; k < splits; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(part + (int64_t)k * n + i);
+    s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
+  }
+  float4 r = make_float4(rv::round_to<__half>(s.x), rv::round_to<__half>(s.y),
+                         rv::round_to<__half>(s.z), rv::round_to<__half>(s.w));
+  float4* o = reinterpret_cast<float4*>(out + i);
+  if (accumulate) {
+    const float4 p = *o;
+    r = make_float4(p.x + r.x, p.y + r.y, p.z + r.z, p.w + r.w);
+  }
+  *o = r;
+}
+
+// dst = fp16(src), round to nearest even; 8 elements per thread.
+__global__ __launch_bounds__(256)
+void cast_f32_f16(const float* __restrict__ src, __half* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * 8;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
+    if (i + 8 <= n) {
+      const float4 a = *reinterpret_cast<const float4*>(src + i);
+      const float4 b = *reinterpret_cast<const float4*>(src + i + 4);
+      const __half2 h0 = __floats2half2_rn(a.x, a.y), h1 = __floats2half2_rn(a.z, a.w);
+      const __half2 h2 = __floats2half2_rn(b.x, b.y), h3 = __floats2half2_rn(b.z, b.w);
+      uint4 v;
+      v.x = *reinterpret_cast<const uint32_t*>(&h0);
+      v.y = *reinterpret_cast<const uint32_t*>(&h1);
+      v.z = *reinterpret_cast<const uint32_t*>(&h2);
+      v.w = *reinterpret_cast<const uint32_t*>(&h3);
+      *reinterpret_cast<uint4*>(dst + i) = v;
+    } else {
+      for (int64_t j = i; j < n; ++j) dst[j] = __float2half_rn(src[j]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Host launch helpers
+// Host side: tile-shape choice and launches.
 // ---------------------------------------------------------------------------
-template <int TM, typename TA, typename TB, bool B_RC, Epi EPI>
-int launch_act(const ActArgs& a, hipStream_t s) {
-  constexpr int BM = 64 * TM;
-  const int64_t cols = (EPI == Epi::SwiGLU) ? 64 : kBN;
-  const int64_t blocks = ((a.m + BM - 1) / BM) * (a.n / cols);
-  hipLaunchKernelGGL((act_gemm<TM, TA, TB, B_RC, EPI>), dim3((unsigned)blocks), dim3(kThreads),
-                     0, s, a);
+struct TileShape {
+  int bm, bn;
+};
+constexpr TileShape kShapes[4] = {{256, 256}, {128, 256}, {128, 128}, {64, 128}};
+
+template <bool A_RC, bool B_RC, Epi EPI>
+int launch(int shape, const GemmArgs& a, int64_t splits, hipStream_t s) {
+  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * splits)), block(kThreads);
+  switch (shape) {
+    case 0: hipLaunchKernelGGL((gemm_kernel<256, 256, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((gemm_kernel<128, 256, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<128, 128, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<64, 128, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
+  }
   return rv_host::check_launch();
 }
 
-bool f16_or_f32(int dt) { return dt == RV_F16 || dt == RV_F32; }
+// Activation GEMMs: C is m x n_out where n_out = n (or n/2 output columns for
+// SwiGLU, whose tile covers bn/2 of them).  The largest tile that gives at
+// least one workgroup per CU; otherwise the one with the most workgroups.
+int pick_act(int64_t m, int64_t n_cols, bool swiglu) {
+  int best = -1;
+  int64_t best_blocks = -1;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t cols = swiglu ? kShapes[i].bn / 2 : kShapes[i].bn;
+    if (n_cols % cols) continue;
+    const int64_t blocks = ((m + kShapes[i].bm - 1) / kShapes[i].bm) * (n_cols / cols);
+    if (blocks >= kCUs) return i;
+    if (blocks > best_blocks) best = i, best_blocks = blocks;
+  }
+  return best;
+}
 
-// Split-K plan for an ni x nj weight gradient over `rows` tokens: enough
-// splits to give ~256 workgroups (at most 16), each split a multiple of kBK
-// tokens.  Depends only on the sizes, so results are device-independent.
+template <bool A_RC, bool B_RC, Epi EPI>
+int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
+  const bool swiglu = EPI == Epi::SwiGLU;
+  const int shape = pick_act(a.m, n_cols, swiglu);
+  if (shape < 0) return RV_ERR_UNSUPPORTED;
+  const TileShape t = kShapes[shape];
+  a.tiles_m = (a.m + t.bm - 1) / t.bm;
+  a.tiles_n = n_cols / (swiglu ? t.bn / 2 : t.bn);
+  a.k_chunk = a.k;
+  return launch<A_RC, B_RC, EPI>(shape, a, 1, s);
+}
+
+// Weight-gradient plan for an ni x nj output reduced over `rows` tokens: tile
+// shape and split count minimising a simple cost (MFMA time at a per-shape
+// efficiency, scaled down when the grid is under one workgroup per CU, plus
+// the partial sums' HBM round trip at ~500 flop per byte).  Depends only on
+// the sizes, so results are device-independent.
 struct WgradPlan {
-  int64_t tiles, splits, chunk;
+  int shape;
+  int64_t tiles_m, tiles_n, splits, chunk;
 };
 WgradPlan plan_wgrad(int64_t rows, int64_t ni, int64_t nj) {
-  WgradPlan p;
-  p.tiles = (ni / 128) * (nj / kBN);
-  int64_t want = 256 / (p.tiles > 0 ? p.tiles : 1);
-  if (want < 1) want = 1;
-  if (want > 16) want = 16;
-  int64_t chunk = (rows + want - 1) / want;
-  chunk = (chunk + kBK - 1) / kBK * kBK;
-  p.chunk = chunk;
-  p.splits = (rows + chunk - 1) / chunk;
-  return p;
+  static const double eff[4] = {0.8, 0.7, 0.5, 0.35};
+  WgradPlan best{-1, 0, 0, 0, 0};
+  double best_cost = 0;
+  for (int i = 0; i < 4; ++i) {
+    const TileShape t = kShapes[i];
+    if (ni % t.bm || nj % t.bn) continue;
+    const int64_t tiles = (ni / t.bm) * (nj / t.bn);
+    int64_t splits = (kCUs + tiles - 1) / tiles;
+    const int64_t max_splits = (rows + 4 * kBK - 1) / (4 * kBK);  // >= 4 stages per split
+    if (splits > max_splits) splits = max_splits;
+    if (splits > 64) splits = 64;
+    if (splits < 1) splits = 1;
+    int64_t chunk = (rows + splits - 1) / splits;
+    chunk = (chunk + kBK - 1) / kBK * kBK;
+    splits = (rows + chunk - 1) / chunk;
+    const double fill = (double)(tiles * splits) / kCUs;
+    const double flops = 2.0 * rows * ni * nj / (eff[i] * (fill < 1 ? fill : 1));
+    const double bytes = splits > 1 ? 8.0 * splits * ni * nj : 0.0;
+    const double cost = flops + 500.0 * bytes;
+    if (best.shape < 0 || cost < best_cost) {
+      best = WgradPlan{i, ni / t.bm, nj / t.bn, splits, chunk};
+      best_cost = cost;
+    }
+  }
+  return best;
 }
+
+int run_wgrad(const __half* a, int64_t lda, const __half* b, int64_t ldb, int64_t rows,
+              int64_t ni, int64_t nj, float* out, int accumulate, float* part, hipStream_t s) {
+  const WgradPlan p = plan_wgrad(rows, ni, nj);
+  if (p.shape < 0) return RV_ERR_UNSUPPORTED;
+  GemmArgs g{};
+  g.a = a; g.lda = lda; g.a_bytes = rows * lda * 2;
+  g.b = b; g.ldb = ldb; g.b_bytes = rows * ldb * 2;
+  g.m = ni; g.n = nj; g.k = rows; g.k_chunk = p.chunk;
+  g.tiles_m = p.tiles_m; g.tiles_n = p.tiles_n;
+  g.ldc = nj; g.accumulate = accumulate;
+  if (p.splits == 1) {
+    g.c = out;
+    return launch<true, true, Epi::AccF32OfF16>(p.shape, g, 1, s);
+  }
+  g.c = part;
+  int st = launch<true, true, Epi::PartialF32>(p.shape, g, p.splits, s);
+  if (st != RV_OK) return st;
+  const int64_t n = ni * nj;
+  hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, part,
+                     (int)p.splits, n, out, accumulate);
+  return rv_host::check_launch();
+}
+
+int64_t wgrad_part_bytes(int64_t rows, int64_t ni, int64_t nj) {
+  const WgradPlan p = plan_wgrad(rows, ni, nj);
+  if (p.shape < 0) return -1;
+  return p.splits > 1 ? p.splits * ni * nj * (int64_t)sizeof(float) : 0;
+}
+
+bool ok16(const void* p) { return rv_host::aligned16(p); }
+
+// Buffer loads address an operand with 32-bit byte offsets.
+bool fits32(int64_t elems) { return elems > 0 && elems * 2 <= (int64_t)INT32_MAX - (int64_t)(1 << 24); }
 
 }  // namespace
 
 extern "C" {
 
-int rv_mlp_up_swiglu(const void* x, int x_dtype, int64_t ldx, const float* w_up,
-                     int64_t rows, int64_t d, int64_t f, void* o, void* u, void* stream) {
+int rv_cast_f32_f16(const float* src, void* dst, int64_t n, void* stream) {
+  if (!src || !dst) return RV_ERR_NULL_POINTER;
+  if (n < 0) return RV_ERR_BAD_SIZE;
+  if (n == 0) return RV_OK;
+  if (!ok16(src) || !ok16(dst)) return RV_ERR_UNSUPPORTED;
+  int64_t blocks = (n + 256 * 8 - 1) / (256 * 8);
+  if (blocks > 8 * kCUs) blocks = 8 * kCUs;
+  hipLaunchKernelGGL(cast_f32_f16, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, src,
+                     static_cast<__half*>(dst), n);
+  return rv_host::check_launch();
+}
+
+int rv_mlp_up_swiglu(const void* x, int64_t ldx, const void* w_up, int64_t rows, int64_t d,
+                     int64_t f, void* o, void* u, void* stream) {
   if (!x || !w_up || !o) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0 || ldx < d) return RV_ERR_BAD_SIZE;
-  if (!f16_or_f32(x_dtype) || d % kBK || f % 64 || ldx % 8) return RV_ERR_UNSUPPORTED;
-  if (!rv_host::aligned16(x) || !rv_host::aligned16(w_up)) return RV_ERR_UNSUPPORTED;
-  ActArgs a{x, ldx, w_up, d, rows, f, d, o, f, u, 2 * f};
-  const hipStream_t s = (hipStream_t)stream;
-  return x_dtype == RV_F32 ? launch_act<2, float, float, false, Epi::SwiGLU>(a, s)
-                           : launch_act<2, __half, float, false, Epi::SwiGLU>(a, s);
+  if (d % kBK || f % 64 || ldx % 8) return RV_ERR_UNSUPPORTED;
+  if (!ok16(x) || !ok16(w_up) || !ok16(o) || (u && !ok16(u))) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * ldx) || !fits32(2 * f * d)) return RV_ERR_UNSUPPORTED;
+  GemmArgs a{};
+  a.a = static_cast<const __half*>(x); a.lda = ldx; a.a_bytes = rows * ldx * 2;
+  a.b = static_cast<const __half*>(w_up); a.ldb = d; a.b_bytes = 2 * f * d * 2;
+  a.m = rows; a.n = 2 * f; a.k = d;
+  a.c = o; a.ldc = f; a.u = u; a.ldu = 2 * f; a.f = f;
+  return run_act<false, false, Epi::SwiGLU>(a, f, (hipStream_t)stream);
 }
 
-int rv_mlp_down(const void* o, const float* w_down, int64_t rows, int64_t d, int64_t f,
-                void* y, void* stream) {
+int rv_mlp_down(const void* o, const void* w_down, int64_t rows, int64_t d, int64_t f, void* y,
+                void* stream) {
   if (!o || !w_down || !y) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0) return RV_ERR_BAD_SIZE;
-  if (f % kBK || d % kBN) return RV_ERR_UNSUPPORTED;
-  if (!rv_host::aligned16(o) || !rv_host::aligned16(w_down)) return RV_ERR_UNSUPPORTED;
-  ActArgs a{o, f, w_down, f, rows, d, f, y, d, nullptr, 0};
-  return launch_act<1, __half, float, false, Epi::StoreF16>(a, (hipStream_t)stream);
+  if (f % kBK || d % 128) return RV_ERR_UNSUPPORTED;
+  if (!ok16(o) || !ok16(w_down) || !ok16(y)) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * f) || !fits32(d * f)) return RV_ERR_UNSUPPORTED;
+  GemmArgs a{};
+  a.a = static_cast<const __half*>(o); a.lda = f; a.a_bytes = rows * f * 2;
+  a.b = static_cast<const __half*>(w_down); a.ldb = f; a.b_bytes = d * f * 2;
+  a.m = rows; a.n = d; a.k = f;
+  a.c = y; a.ldc = d;
+  return run_act<false, false, Epi::StoreF16>(a, d, (hipStream_t)stream);
 }
 
-int rv_mlp_dgate(const void* dy, const float* w_down, const void* u, int64_t rows, int64_t d,
+int rv_mlp_dgate(const void* dy, const void* w_down, const void* u, int64_t rows, int64_t d,
                  int64_t f, void* du, void* stream) {
   if (!dy || !w_down || !u || !du) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0) return RV_ERR_BAD_SIZE;
-  if (d % kBK || f % kBN) return RV_ERR_UNSUPPORTED;
-  if (!rv_host::aligned16(dy) || !rv_host::aligned16(w_down)) return RV_ERR_UNSUPPORTED;
-  ActArgs a{dy, d, w_down, f, rows, f, d, du, 2 * f, const_cast<void*>(u), 2 * f};
-  return launch_act<2, __half, float, true, Epi::SwiGLUBwd>(a, (hipStream_t)stream);
+  if (d % kBK || f % 128) return RV_ERR_UNSUPPORTED;
+  if (!ok16(dy) || !ok16(w_down)) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * d) || !fits32(d * f)) return RV_ERR_UNSUPPORTED;
+  GemmArgs a{};
+  a.a = static_cast<const __half*>(dy); a.lda = d; a.a_bytes = rows * d * 2;
+  a.b = static_cast<const __half*>(w_down); a.ldb = f;  // B(f, d) = W_down[d][f]: RC
+  a.b_bytes = d * f * 2;
+  a.m = rows; a.n = f; a.k = d;
+  a.c = du; a.ldc = 2 * f; a.u = const_cast<void*>(u); a.ldu = 2 * f; a.f = f;
+  return run_act<false, true, Epi::SwiGLUBwd>(a, f, (hipStream_t)stream);
 }
 
-int rv_mlp_dx(const void* du, const float* w_up, int64_t rows, int64_t d, int64_t f,
-              float* dx, void* stream) {
+int rv_mlp_dx(const void* du, const void* w_up, int64_t rows, int64_t d, int64_t f, float* dx,
+              void* stream) {
   if (!du || !w_up || !dx) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0) return RV_ERR_BAD_SIZE;
-  if ((2 * f) % kBK || d % kBN) return RV_ERR_UNSUPPORTED;
-  if (!rv_host::aligned16(du) || !rv_host::aligned16(w_up)) return RV_ERR_UNSUPPORTED;
-  ActArgs a{du, 2 * f, w_up, d, rows, d, 2 * f, dx, d, nullptr, 0};
-  return launch_act<1, __half, float, true, Epi::StoreF32OfF16>(a, (hipStream_t)stream);
+  if ((2 * f) % kBK || d % 128) return RV_ERR_UNSUPPORTED;
+  if (!ok16(du) || !ok16(w_up)) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * 2 * f) || !fits32(2 * f * d)) return RV_ERR_UNSUPPORTED;
+  GemmArgs a{};
+  a.a = static_cast<const __half*>(du); a.lda = 2 * f; a.a_bytes = rows * 2 * f * 2;
+  a.b = static_cast<const __half*>(w_up); a.ldb = d;  // B(d, j) = W_up[j][d]: RC
+  a.b_bytes = 2 * f * d * 2;
+  a.m = rows; a.n = d; a.k = 2 * f;
+  a.c = dx; a.ldc = d;
+  return run_act<false, true, Epi::StoreF32OfF16>(a, d, (hipStream_t)stream);
 }
 
 int64_t rv_mlp_wgrad_workspace_bytes(int64_t rows, int64_t d, int64_t f) {
   if (rows <= 0 || d <= 0 || f <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
-  const WgradPlan pd = plan_wgrad(rows, d, f), pu = plan_wgrad(rows, 2 * f, d);
-  const int64_t a = pd.splits * d * f, b = pu.splits * 2 * f * d;
-  return (a > b ? a : b) * (int64_t)sizeof(float);
+  const int64_t a = wgrad_part_bytes(rows, d, f), b = wgrad_part_bytes(rows, 2 * f, d);
+  if (a < 0 || b < 0) return -(int64_t)RV_ERR_UNSUPPORTED;
+  return a > b ? a : b;
 }
 
-int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x, int x_dtype,
-                 int64_t ldx, int64_t rows, int64_t d, int64_t f, float* ddown, float* dup,
-                 int accumulate, void* workspace, int64_t workspace_bytes, void* stream) {
+int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x, int64_t ldx,
+                 int64_t rows, int64_t d, int64_t f, float* ddown, float* dup, int accumulate,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
   if (!dy || !o || !du || !x || !ddown || !dup) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0 || ldx < d) return RV_ERR_BAD_SIZE;
-  if (!f16_or_f32(x_dtype) || d % kBN || f % kBN || ldx % 8) return RV_ERR_UNSUPPORTED;
+  if (d % 128 || f % 128 || ldx % 8) return RV_ERR_UNSUPPORTED;
+  if (!ok16(dy) || !ok16(o) || !ok16(du) || !ok16(x) || !ok16(ddown) || !ok16(dup))
+    return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * 2 * f) || !fits32(rows * ldx) || !fits32(rows * f)) return RV_ERR_UNSUPPORTED;
   const int64_t need = rv_mlp_wgrad_workspace_bytes(rows, d, f);
-  if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
+  if (need < 0) return (int)-need;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !ok16(workspace)))
+    return RV_ERR_WORKSPACE;
   const hipStream_t s = (hipStream_t)stream;
   float* part = static_cast<float*>(workspace);
   // dW_down[d][f] = sum_m dy[m][d] o[m][f]
-  {
-    const WgradPlan p = plan_wgrad(rows, d, f);
-    WgradArgs a{dy, d, o, f, rows, d, f, p.chunk, part};
-    hipLaunchKernelGGL((wgrad_gemm<__half, __half>), dim3((unsigned)(p.splits * p.tiles)),
-                       dim3(kThreads), 0, s, a);
-    int st = rv_host::check_launch();
-    if (st != RV_OK) return st;
-    const int64_t n = d * f;
-    hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part,
-                       (int)p.splits, n, ddown, accumulate);
-    st = rv_host::check_launch();
-    if (st != RV_OK) return st;
-  }
+  int st = run_wgrad(static_cast<const __half*>(dy), d, static_cast<const __half*>(o), f, rows,
+                     d, f, ddown, accumulate, part, s);
+  if (st != RV_OK) return st;
   // dW_up[2f][d] = sum_m du[m][j] x16[m][d]
-  {
-    const WgradPlan p = plan_wgrad(rows, 2 * f, d);
-    WgradArgs a{du, 2 * f, x, ldx, rows, 2 * f, d, p.chunk, part};
-    if (x_dtype == RV_F32)
-      hipLaunchKernelGGL((wgrad_gemm<__half, float>), dim3((unsigned)(p.splits * p.tiles)),
-                         dim3(kThreads), 0, s, a);
-    else
-      hipLaunchKernelGGL((wgrad_gemm<__half, __half>), dim3((unsigned)(p.splits * p.tiles)),
-                         dim3(kThreads), 0, s, a);
-    int st = rv_host::check_launch();
-    if (st != RV_OK) return st;
-    const int64_t n = 2 * f * d;
-    hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, part,
-                       (int)p.splits, n, dup, accumulate);
-    return rv_host::check_launch();
-  }
+  return run_wgrad(static_cast<const __half*>(du), 2 * f, static_cast<const __half*>(x), ldx,
+                   rows, 2 * f, d, dup, accumulate, part, s);
 }
 
 }  // extern "C"

@@ -1,25 +1,27 @@
 """MFMA MLP projections with fused SwiGLU epilogues (the HIP path of TiledMLP).
 
 Thin launchers over the C ABI (``rv_mlp_*`` in include/reversibility_hip.h) for
-one token tile of the SwiGLU MLP under fp16 autocast:
+one token tile of the SwiGLU MLP under fp16 autocast.  All operands are fp16:
 
-    up_swiglu(x, W_up)          o = fp16(silu(fp16 u_g)) * fp16 u_v, u = x16 W_up16^T
-    down(o, W_down, out)        out = fp16(o W_down16^T)
-    dgate(dy, W_down, u)        du = swiglu_bwd(u, fp16(dy W_down16))
-    dx(du, W_up, out)           out = fp32(fp16(du W_up16))
-    wgrad(dy, o, du, x, ...)    dW_down (+)= fp32(fp16(dy^T o)), dW_up (+)= fp32(fp16(du^T x16))
+    cast_f16(t)                 fp16 copy of an fp32 tensor (autocast's cast)
+    up_swiglu(x, W_up)          o = fp16(silu(fp16 u_g)) * fp16 u_v, u = x W_up^T
+    down(o, W_down, out)        out = fp16(o W_down^T)
+    dgate(dy, W_down, u)        du = swiglu_bwd(u, fp16(dy W_down))
+    dx(du, W_up, out)           out = fp32(fp16(du W_up))
+    wgrad(dy, o, du, x, ...)    dW_down (+)= fp32(fp16(dy^T o)), dW_up (+)= fp32(fp16(du^T x))
 
-fp32 operands (weights, normalized activations) are cast to fp16 inside the
-kernels' loads -- autocast's cast, without a separate kernel.  Outputs are
-written into caller-provided slices where the tiled caller owns the buffer.
-``supported`` says whether a shape is covered (model width and hidden width
-multiples of 128); the caller uses torch's GEMMs otherwise.
+The weights passed here are the fp16 casts of the fp32 masters (one cast per
+TiledMLP call: autocast's F.linear casts the same fp32 weight to the same fp16
+values on every call).  Outputs are written into caller-provided slices where
+the tiled caller owns the buffer.  ``supported`` says whether a shape is
+covered (model width and hidden width multiples of 128); the caller uses
+torch's GEMMs otherwise.
 """
 from __future__ import annotations
 
 import torch
 
-from ._hip import RV_F16, RV_F32, _check, _stream, library
+from ._hip import _check, _stream, library
 
 
 def supported(x: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> bool:
@@ -31,23 +33,38 @@ def supported(x: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> bool:
             and d % 128 == 0 and f % 128 == 0)
 
 
-def _xcode(x):
-    return RV_F32 if x.dtype == torch.float32 else RV_F16
+def cast_f16(t: torch.Tensor) -> torch.Tensor:
+    """fp16 copy of a contiguous fp32 tensor (round to nearest even); fp16 passes through."""
+    if t.dtype == torch.float16:
+        return t.contiguous()
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError("cast_f16 needs a contiguous fp32 or fp16 CUDA (ROCm device) tensor")
+    out = torch.empty(t.shape, device=t.device, dtype=torch.float16)
+    _check(library().rv_cast_f32_f16(t.data_ptr(), out.data_ptr(), t.numel(), _stream(t)),
+           "rv_cast_f32_f16")
+    return out
+
+
+def _f16(t: torch.Tensor, what: str) -> None:
+    if t.dtype != torch.float16:
+        raise ValueError(f"{what} must be fp16 (cast with mlp.cast_f16)")
 
 
 def up_swiglu(x: torch.Tensor, up: torch.Tensor, keep_u: bool = False):
-    """x [rows, d] fp32/fp16 (contiguous rows), up [2f, d] fp32 -> (o, u or None)."""
+    """x [rows, d] fp16 (contiguous rows), up [2f, d] fp16 -> (o, u or None)."""
+    _f16(x, "x"), _f16(up, "W_up")
     rows, d = x.shape
     f = up.shape[0] // 2
     o = torch.empty(rows, f, device=x.device, dtype=torch.float16)
     u = torch.empty(rows, 2 * f, device=x.device, dtype=torch.float16) if keep_u else None
-    _check(library().rv_mlp_up_swiglu(x.data_ptr(), _xcode(x), x.stride(0), up.data_ptr(), rows, d,
-                                      f, o.data_ptr(), u.data_ptr() if keep_u else None,
+    _check(library().rv_mlp_up_swiglu(x.data_ptr(), x.stride(0), up.data_ptr(), rows, d, f,
+                                      o.data_ptr(), u.data_ptr() if keep_u else None,
                                       _stream(x)), "rv_mlp_up_swiglu")
     return o, u
 
 
 def down(o: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    _f16(o, "o"), _f16(w, "W_down")
     rows, f = o.shape
     d = w.shape[0]
     _check(library().rv_mlp_down(o.data_ptr(), w.data_ptr(), rows, d, f, out.data_ptr(),
@@ -56,6 +73,7 @@ def down(o: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
 
 
 def dgate(dy: torch.Tensor, w_down: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    _f16(dy, "dy"), _f16(w_down, "W_down"), _f16(u, "u")
     rows, d = dy.shape
     f = w_down.shape[1]
     du = torch.empty(rows, 2 * f, device=dy.device, dtype=torch.float16)
@@ -65,6 +83,7 @@ def dgate(dy: torch.Tensor, w_down: torch.Tensor, u: torch.Tensor) -> torch.Tens
 
 
 def dx(du: torch.Tensor, w_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    _f16(du, "du"), _f16(w_up, "W_up")
     rows, two_f = du.shape
     d = w_up.shape[1]
     _check(library().rv_mlp_dx(du.data_ptr(), w_up.data_ptr(), rows, d, two_f // 2,
@@ -73,13 +92,15 @@ def dx(du: torch.Tensor, w_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
 
 
 def wgrad(dy, o, du, x, ddown, dup, accumulate: bool) -> None:
+    for t, what in ((dy, "dy"), (o, "o"), (du, "du"), (x, "x")):
+        _f16(t, what)
     rows, d = dy.shape
     f = o.shape[1]
     lib = library()
     nbytes = lib.rv_mlp_wgrad_workspace_bytes(rows, d, f)
     if nbytes < 0:
         _check(-nbytes, "rv_mlp_wgrad_workspace_bytes")
-    ws = torch.empty(nbytes // 4, device=dy.device, dtype=torch.float32)
-    _check(lib.rv_mlp_wgrad(dy.data_ptr(), o.data_ptr(), du.data_ptr(), x.data_ptr(), _xcode(x),
+    ws = torch.empty(max(nbytes, 4) // 4, device=dy.device, dtype=torch.float32)
+    _check(lib.rv_mlp_wgrad(dy.data_ptr(), o.data_ptr(), du.data_ptr(), x.data_ptr(),
                             x.stride(0), rows, d, f, ddown.data_ptr(), dup.data_ptr(),
                             int(accumulate), ws.data_ptr(), nbytes, _stream(dy)), "rv_mlp_wgrad")

@@ -111,10 +111,14 @@ class TiledMLP(torch.autograd.Function):
         output = torch.empty((flat.shape[0], down.shape[0]), device=x.device, dtype=cdt)
         if _use_mfma(flat, up, down, fused, cdt):
             from . import mlp
-            flat = flat.contiguous()
+            # autocast's casts, once per call: the same fp16 values F.linear
+            # would produce on every tile
+            x16 = mlp.cast_f16(flat.contiguous())
+            up16, down16 = mlp.cast_f16(up), mlp.cast_f16(down)
             for start in range(0, flat.shape[0], tokens):
-                o, _ = mlp.up_swiglu(flat[start:start + tokens], up)
-                mlp.down(o, down, output[start:start + tokens])
+                o, _ = mlp.up_swiglu(x16[start:start + tokens], up16)
+                mlp.down(o, down16, output[start:start + tokens])
+            del x16, up16, down16
             ctx.save_for_backward(x, up, down)
             return output.reshape(*x.shape[:-1], down.shape[0])
         with torch.autocast(ctx.device, enabled=False):
@@ -137,14 +141,15 @@ class TiledMLP(torch.autograd.Function):
         dx = torch.empty_like(flat)
         if _use_mfma(flat, up, down, ctx.fused, cdt):
             from . import mlp
-            flat, dy = flat.contiguous(), dy.contiguous()
+            x16, dy = mlp.cast_f16(flat.contiguous()), dy.contiguous()
+            up16, down16 = mlp.cast_f16(up), mlp.cast_f16(down)
             dup, ddown = torch.empty_like(up), torch.empty_like(down)
             for i, start in enumerate(range(0, flat.shape[0], ctx.tokens)):
                 stop = start + ctx.tokens
-                x_t, g = flat[start:stop], dy[start:stop]
-                o, u = mlp.up_swiglu(x_t, up, keep_u=True)
-                du = mlp.dgate(g, down, u)
-                mlp.dx(du, up, dx[start:stop])
+                x_t, g = x16[start:stop], dy[start:stop]
+                o, u = mlp.up_swiglu(x_t, up16, keep_u=True)
+                du = mlp.dgate(g, down16, u)
+                mlp.dx(du, up16, dx[start:stop])
                 mlp.wgrad(g, o, du, x_t, ddown, dup, accumulate=i > 0)
                 del o, u, du
             return dx.reshape_as(x), dup, ddown, None, None

@@ -10,6 +10,11 @@ its final fp16 rounding, so the bar per element is
 
 plus relative-L2 agreement (1e-3).  The SwiGLU parts are checked against the
 CPU oracle applied to the kernel's own pre-activations.
+
+The shapes make every tile shape the library chooses (256x256, 128x256,
+128x128, 64x128) serve every epilogue at least once, and the weight gradients
+take both the direct-accumulate and the split-K path; the 8192 x 1024 x 4096
+case is one configs[4] token tile.
 """
 from __future__ import annotations
 
@@ -23,29 +28,37 @@ from reversability_amd import mlp
 pytestmark = pytest.mark.gpu
 
 
+def fp16_ulp(t: torch.Tensor) -> torch.Tensor:
+    """Spacing of fp16 at |t| (2^-24 below the normal range), on t's device."""
+    a = t.abs().double()
+    e = torch.floor(torch.log2(a.clamp_min(2.0 ** -14))).clamp_min(-14)
+    return torch.pow(2.0, e - 10)
+
+
 def ulps(actual: torch.Tensor, expected: torch.Tensor) -> torch.Tensor:
     e = expected.float()
     ulp = torch.from_numpy(np.spacing(np.abs(e.cpu().numpy()).astype(np.float16)).astype(np.float32))
     return (actual.float().cpu() - e.cpu()).abs() / ulp
 
 
+def rel_l2(a, b):
+    a, b = a.double(), b.double().to(a.device)
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
 def within_gemm_bound(out, a, b, k, transpose_b=True):
-    """out vs fp64 truth of a @ b^T (or a @ b) with the bound in the module docstring."""
-    a64, b64 = a.double().cpu(), b.double().cpu()
+    """out vs the fp64 truth of a @ b^T (or a @ b), computed on out's device,
+    with the bound in the module docstring."""
+    a64, b64 = a.double().to(out.device), b.double().to(out.device)
     bt = b64.t() if transpose_b else b64
     truth = a64 @ bt
     scale = a64.abs() @ bt.abs()
-    ulp = torch.from_numpy(np.spacing(np.abs(truth.numpy()).astype(np.float16)).astype(np.float64))
-    err = (out.double().cpu() - truth).abs()
-    bound = ulp + k * 2.0 ** -24 * scale
+    err = (out.double() - truth).abs()
+    bound = fp16_ulp(truth) + k * 2.0 ** -24 * scale
     worst = float((err / bound).max())
-    print(f"  worst error / bound = {worst:.3f}, rel_l2 = {rel_l2(out, truth):.2e}", flush=True)
-    return worst <= 1.0 and rel_l2(out, truth) < 1e-3
-
-
-def rel_l2(a, b):
-    a, b = a.double().cpu(), b.double().cpu()
-    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+    r = rel_l2(out, truth)
+    print(f"  worst error / bound = {worst:.3f}, rel_l2 = {r:.2e}", flush=True)
+    return worst <= 1.0 and r < 1e-3
 
 
 def weights(d, f, dev, seed=1337):
@@ -55,23 +68,36 @@ def weights(d, f, dev, seed=1337):
     return up.to(dev), down.to(dev)
 
 
-SHAPES = [(8192, 256, 1024), (6656, 256, 1024), (17, 256, 1024), (1000, 1024, 4096)]
+SHAPES = [(8192, 256, 1024), (6656, 256, 1024), (17, 256, 1024), (1000, 1024, 4096),
+          (8192, 1024, 4096), (16384, 256, 1024), (16384, 1024, 4096)]
+
+
+def test_cast_f16_matches_torch(cuda_device):
+    g = torch.Generator().manual_seed(9)
+    for n in (1, 7, 8, 4096 + 3, 1 << 20):
+        x = (torch.randn(n, generator=g) * 1e3).to(cuda_device)
+        x[: min(n, 4)] = torch.tensor([65520.0, -65504.0, 6e-8, float("nan")][: min(n, 4)])
+        y = mlp.cast_f16(x)
+        ref = x.half()
+        assert torch.equal(torch.isnan(y), torch.isnan(ref))
+        keep = ~torch.isnan(ref)
+        assert torch.equal(y[keep], ref[keep]), n
 
 
 @pytest.mark.parametrize("rows,d,f", SHAPES)
-@pytest.mark.parametrize("xdt", [torch.float32, torch.float16])
-def test_up_swiglu(cuda_device, rows, d, f, xdt):
+def test_up_swiglu(cuda_device, rows, d, f):
     up, _ = weights(d, f, cuda_device)
-    x = torch.randn(rows, d, generator=torch.Generator().manual_seed(1), dtype=torch.float32).to(cuda_device).to(xdt)
-    o, u = mlp.up_swiglu(x, up, keep_u=True)
-    assert within_gemm_bound(u, x.half(), up.half(), d)
-    u_ref = (x.half().float() @ up.half().float().t()).half()
+    x = torch.randn(rows, d, generator=torch.Generator().manual_seed(1)).to(cuda_device)
+    x16, up16 = mlp.cast_f16(x), mlp.cast_f16(up)
+    o, u = mlp.up_swiglu(x16, up16, keep_u=True)
+    assert within_gemm_bound(u, x16, up16, d)
+    u_ref = (x16.float() @ up16.float().t()).half()
     o_ref = torch.from_numpy(oracle.swiglu_fwd(u_ref.cpu().numpy()))
-    assert rel_l2(o, o_ref) < 2e-3
+    assert rel_l2(o.cpu(), o_ref) < 2e-3
     # given the kernel's own u, o is the SwiGLU of it (same epilogue rounding)
     o_own = torch.from_numpy(oracle.swiglu_fwd(u.cpu().numpy()))
     assert float(ulps(o, o_own).max()) <= 2.0
-    o2, _ = mlp.up_swiglu(x, up)
+    o2, _ = mlp.up_swiglu(x16, up16)
     assert torch.equal(o, o2)  # deterministic, u output optional
 
 
@@ -80,22 +106,25 @@ def test_down(cuda_device, rows, d, f):
     _, down = weights(d, f, cuda_device)
     o = (0.5 * torch.randn(rows, f, generator=torch.Generator().manual_seed(2))).half().to(cuda_device)
     y = torch.empty(rows, d, device=cuda_device, dtype=torch.float16)
-    mlp.down(o, down, y)
-    assert within_gemm_bound(y, o, down.half(), f)
+    down16 = mlp.cast_f16(down)
+    mlp.down(o, down16, y)
+    assert within_gemm_bound(y, o, down16, f)
 
 
 @pytest.mark.parametrize("rows,d,f", SHAPES)
 def test_dgate(cuda_device, rows, d, f):
-    up, down = weights(d, f, cuda_device)
+    _, down = weights(d, f, cuda_device)
     g = torch.Generator().manual_seed(3)
     dy = torch.randn(rows, d, generator=g).half().to(cuda_device)
     u = torch.randn(rows, 2 * f, generator=g).half().to(cuda_device)
-    du = mlp.dgate(dy, down, u)
-    d_o = (dy.float() @ down.half().float()).half()
+    down16 = mlp.cast_f16(down)
+    du = mlp.dgate(dy, down16, u)
+    d_o = (dy.float() @ down16.float()).half()
     du_ref = torch.from_numpy(oracle.swiglu_bwd(u.cpu().numpy(), d_o.cpu().numpy()))
-    print(f"  rel_l2 = {rel_l2(du, du_ref):.2e}, >2ulp frac = {float((ulps(du, du_ref) > 2).float().mean()):.2e}")
-    assert rel_l2(du, du_ref) < 2e-3
-    assert (ulps(du, du_ref) > 2).float().mean() < 0.01
+    frac = float((ulps(du, du_ref) > 2).float().mean())
+    print(f"  rel_l2 = {rel_l2(du.cpu(), du_ref):.2e}, >2ulp frac = {frac:.2e}")
+    assert rel_l2(du.cpu(), du_ref) < 2e-3
+    assert frac < 0.01
 
 
 @pytest.mark.parametrize("rows,d,f", SHAPES)
@@ -103,10 +132,11 @@ def test_dx(cuda_device, rows, d, f):
     up, _ = weights(d, f, cuda_device)
     du = (0.3 * torch.randn(rows, 2 * f, generator=torch.Generator().manual_seed(4))).half().to(cuda_device)
     dx = torch.empty(rows, d, device=cuda_device)
-    mlp.dx(du, up, dx)
+    up16 = mlp.cast_f16(up)
+    mlp.dx(du, up16, dx)
     assert dx.dtype == torch.float32
     assert torch.equal(dx, dx.half().float())  # an fp16 value widened
-    assert within_gemm_bound(dx, du, up.half(), 2 * f, transpose_b=False)
+    assert within_gemm_bound(dx, du, up16, 2 * f, transpose_b=False)
 
 
 @pytest.mark.parametrize("rows,d,f", SHAPES)
@@ -115,12 +145,22 @@ def test_wgrad_and_accumulate(cuda_device, rows, d, f):
     dy = torch.randn(rows, d, generator=g).half().to(cuda_device)
     o = torch.randn(rows, f, generator=g).half().to(cuda_device)
     du = (0.3 * torch.randn(rows, 2 * f, generator=g)).half().to(cuda_device)
-    x = torch.randn(rows, d, generator=g).to(cuda_device)
+    x16 = torch.randn(rows, d, generator=g).half().to(cuda_device)
     ddown = torch.empty(d, f, device=cuda_device)
     dup = torch.empty(2 * f, d, device=cuda_device)
-    mlp.wgrad(dy, o, du, x, ddown, dup, accumulate=False)
+    mlp.wgrad(dy, o, du, x16, ddown, dup, accumulate=False)
+    assert torch.equal(ddown, ddown.half().float()) and torch.equal(dup, dup.half().float())
     assert within_gemm_bound(ddown, dy.t(), o.t(), rows)
-    assert within_gemm_bound(dup, du.t(), x.half().t(), rows)
+    assert within_gemm_bound(dup, du.t(), x16.t(), rows)
     first = (ddown.clone(), dup.clone())
-    mlp.wgrad(dy, o, du, x, ddown, dup, accumulate=True)
+    mlp.wgrad(dy, o, du, x16, ddown, dup, accumulate=True)
     assert torch.equal(ddown, first[0] + first[0]) and torch.equal(dup, first[1] + first[1])
+
+
+def test_rejects_fp32_operands(cuda_device):
+    up, down = weights(256, 1024, cuda_device)
+    x = torch.randn(64, 256, device=cuda_device)
+    with pytest.raises(ValueError, match="fp16"):
+        mlp.up_swiglu(x, mlp.cast_f16(up))
+    with pytest.raises(ValueError, match="fp16"):
+        mlp.up_swiglu(x.half(), up)
