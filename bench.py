@@ -224,16 +224,27 @@ TRAIN_CONFIGS = {
 }
 
 
+# Cached-head token chunk: the reference probes 1024 on a 16 GB T4
+# (scripts/benchmark_midpoint_v3.py:174); on a 288 GB MI355X one chunk covers
+# the whole batch (C4 logits: 1.7 GB fp16), measured fastest (C4 14.7 ms vs
+# 19.4 ms at 1024).  None = the whole batch.
+HEAD_CHUNK = None
+
+
 def make_train_step(dev, name: str):
-    """One full training update of a TRAIN_CONFIGS entry: fp16 autocast forward,
-    sum cross-entropy over the batch / valid targets, reconstruction backward,
-    GradScaler unscale, clip 1.0, AdamW (0.9, 0.95), wd 0.1.  Returns
-    (step function returning the summed loss, targets per step, config)."""
+    """One full training update of a TRAIN_CONFIGS entry, on the reference's
+    v3 probe path (scripts/benchmark_midpoint_v3.py:78-83 over
+    scripts/benchmark_optimized.py:54-82): install_v3 (split core for the
+    midpoint config, 8192-token tiled MLP, fused SwiGLU and RMSNorm), then
+    cached_head_backward -- fp16 autocast core forward, the tied head and the
+    fused cross-entropy in HEAD_CHUNK-token chunks, sum loss / valid targets, one
+    core backward -- then GradScaler unscale, clip 1.0 and AdamW (0.9, 0.95),
+    wd 0.1.  Returns (step function returning the summed loss, targets per
+    step, config)."""
     import numpy as np
     import torch
-    import torch.nn.functional as F
     from reversability_amd import build_model
-    from reversability_amd.optimized_v3 import install_v3
+    from reversability_amd.optimized_v3 import cached_head_backward, install_v3
 
     cfg = TRAIN_CONFIGS[name]
     batch, length = cfg["batch"], cfg["model"]["max_sequence_length"]
@@ -252,10 +263,8 @@ def make_train_step(dev, name: str):
 
     def step():
         opt.zero_grad(set_to_none=True)
-        with torch.autocast("cuda", dtype=torch.float16):
-            logits = model(x)
-            loss = F.cross_entropy(logits.flatten(0, 1), y.flatten(), reduction="sum")
-            scaler.scale(loss / targets).backward()
+        loss = cached_head_backward(model, x, y, targets, HEAD_CHUNK or targets, scaler, "fp16",
+                                    False, "triton")
         scaler.unscale_(opt)
         torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
         scaler.step(opt)
@@ -282,6 +291,8 @@ def train_step_bench(dev, steps: int, warmup: int, name: str = "c4"):
             "config": {"workload": cfg["workload"], "global_batch": cfg["batch"],
                        "seq_len": cfg["model"]["max_sequence_length"],
                        "core_mode": cfg["core_mode"], "mlp_tokens": 8192,
+                       "head": f"cached head, {HEAD_CHUNK or 'whole-batch'} token chunks, "
+                               "fused CE",
                        "precision": "fp16-autocast"},
             "data": "synthetic uniform token ids (seed 1337)"}
 

@@ -207,6 +207,30 @@ int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x,
                  float* ddown, float* dup, int accumulate, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Cross-entropy over vocabulary rows (the tied LM head's loss).
+ * logits [rows, ld] fp16 (RV_F16) or fp32 (RV_F32), first cols columns used;
+ * labels int64 [rows]; rows whose label equals ignore_index contribute 0.
+ * Replace TiledCrossEntropy's _ce_partials / _ce_rows / _ce_grad launches
+ * (src/reversibility/kernels.py:14-77).
+ */
+
+/* row_max = max_j x_j, row_lse = log(sum_j exp(x_j - row_max)) and
+ * loss = -round_T((x_t - row_max) - row_lse), all fp32 [rows]; a label
+ * outside [0, cols) other than ignore_index gives a NaN loss. */
+int rv_ce_fwd(const void* logits, int dtype, int64_t ld, const int64_t* labels,
+              int64_t rows, int64_t cols, int64_t ignore_index, float* row_max,
+              float* row_lse, float* loss, void* stream);
+
+/* dlogits (layout and dtype of logits) = gradient of sum(loss) times *grad
+ * (a device fp32 scalar): round_T([j == t] n - exp(round_T((x_j - row_max) -
+ * row_lse)) n), n = round_T(-*grad); zero rows for ignore_index.  logits and
+ * dlogits must share their address modulo 16. */
+int rv_ce_bwd(const void* logits, int dtype, int64_t ld, const int64_t* labels,
+              const float* row_max, const float* row_lse, const float* grad,
+              int64_t rows, int64_t cols, int64_t ignore_index, void* dlogits,
+              void* stream);
+
 #ifdef __cplusplus
 }
 #endif

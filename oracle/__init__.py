@@ -11,7 +11,8 @@ Contents
     :func:`rmsnorm_fwd`, :func:`rmsnorm_bwd` (src/reversibility/kernels_v3.py:9-48),
     :func:`swiglu_fwd`, :func:`swiglu_bwd` (src/reversibility/kernels.py:88-110),
     :func:`midpoint`, :func:`midpoint_bwd`, :func:`euler`
-    (src/reversibility/reversible.py:16-32).
+    (src/reversibility/reversible.py:16-32), :func:`ce_fwd`, :func:`ce_bwd`
+    (src/reversibility/kernels.py:14-77).
 ``model_ref.py``
     torch-CPU functional restatement of the decoder and both integrators
     (src/reversibility/model.py, reversible.py) for model-level checks.
@@ -24,6 +25,10 @@ How each function is pinned (tests/test_oracle.py):
         fp64 autograd of silu(g)*v at fp16 tolerance, special values
         (g = 0, large |g|), golden file.
     midpoint/euler  -- torch's own eager fp16/fp32 expression bit for bit.
+    ce_fwd/bwd      -- fp64 cross-entropy and its gradient (library), the
+        uniform-logits closed form log V, torch's eager fp16 log_softmax at
+        the target (the reference's Half-logsoftmax policy), zero column sums
+        of the gradient, ignore_index rows.
     f16 conversion  -- all 65536 binary16 patterns round-trip; numpy's
         float16 cast on 2^20 random floats including subnormals/overflow.
 """
@@ -72,6 +77,8 @@ def lib() -> ctypes.CDLL:
             "oracle_euler": (None, [P, P, P, I, I64, I]),
             "oracle_f32_to_f16_array": (None, [P, P, I64]),
             "oracle_f16_to_f32_array": (None, [P, P, I64]),
+            "oracle_ce_fwd": (None, [P, I64, P, I64, I64, I64, I, P, P, P]),
+            "oracle_ce_bwd": (None, [P, I64, P, P, P, F, I64, I64, I64, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -199,3 +206,28 @@ def f16_bits_to_f32(b: np.ndarray) -> np.ndarray:
     out = np.empty(b.shape, np.float32)
     lib().oracle_f16_to_f32_array(_ptr(b), _ptr(out), b.size)
     return out
+
+
+def ce_fwd(x: np.ndarray, labels: np.ndarray, ignore_index: int = -100):
+    """(row_max, row_lse, loss) float32 [rows] for logits x [rows, cols] float16/float32."""
+    x = np.ascontiguousarray(x)
+    labels = np.ascontiguousarray(labels, np.int64)
+    rows, cols = x.shape
+    rmax, rlse, loss = (np.empty(rows, np.float32) for _ in range(3))
+    lib().oracle_ce_fwd(_ptr(x), cols, _ptr(labels), rows, cols, ignore_index, _code(x),
+                        _ptr(rmax), _ptr(rlse), _ptr(loss))
+    return rmax, rlse, loss
+
+
+def ce_bwd(x: np.ndarray, labels: np.ndarray, rmax: np.ndarray, rlse: np.ndarray, grad: float,
+           ignore_index: int = -100) -> np.ndarray:
+    """d(sum loss)/dx * grad, in x's dtype, given the forward's row statistics."""
+    x = np.ascontiguousarray(x)
+    labels = np.ascontiguousarray(labels, np.int64)
+    rmax = np.ascontiguousarray(rmax, np.float32)
+    rlse = np.ascontiguousarray(rlse, np.float32)
+    rows, cols = x.shape
+    dx = np.empty_like(x)
+    lib().oracle_ce_bwd(_ptr(x), cols, _ptr(labels), _ptr(rmax), _ptr(rlse), grad, rows, cols,
+                        ignore_index, _code(x), _ptr(dx))
+    return dx

@@ -14,6 +14,10 @@
  *   oracle_midpoint      src/reversibility/reversible.py:16-32  (p +/- 2h (A+M))
  *   oracle_midpoint_bwd  autograd of the same eager expression
  *   oracle_euler         src/reversibility/reversible.py:24-25,31-32
+ *   oracle_ce_fwd        src/reversibility/kernels.py:14-45,56-67 (_ce_partials,
+ *                        _ce_rows, TiledCrossEntropy.forward)
+ *   oracle_ce_bwd        src/reversibility/kernels.py:48-60,69-77 (_ce_grad,
+ *                        TiledCrossEntropy.backward)
  *
  * RMSNorm sums are accumulated in double (a tighter reference than any fp32
  * summation order); outputs are rounded once to float.  SwiGLU uses float
@@ -286,4 +290,70 @@ void oracle_f32_to_f16_array(const float* src, uint16_t* dst, int64_t n) {
 
 void oracle_f16_to_f32_array(const uint16_t* src, float* dst, int64_t n) {
   for (int64_t i = 0; i < n; ++i) dst[i] = oracle_f16_to_f32(src[i]);
+}
+
+/* ---- tiled cross-entropy (src/reversibility/kernels.py:14-71) ----------
+ * Per row of logits x (fp16 bits or float, row stride ld):
+ *   maximum     m   = max_j x_j                                  (exact)
+ *   denominator lse = log(sum_j exp(x_j - m)), accumulated in double,
+ *                     rounded once to float                      (_ce_rows)
+ *   logp        = round_T((x_t - m) - lse)     float arithmetic, then the
+ *                                              logits dtype T    (_ce_rows)
+ *   loss        = -logp, 0 for label == ignore
+ *   dx_j        = round_T([j == t] neg - exp(round_T((x_j - m) - lse)) neg),
+ *                 neg = round_T(-grad), 0 rows for ignore         (_ce_grad)
+ * A label outside [0, cols) other than ignore gives a NaN loss / NaN row. */
+static inline float load_logit(const void* x, int64_t i, int dtype) {
+  return dtype == F16 ? oracle_f16_to_f32(((const uint16_t*)x)[i]) : ((const float*)x)[i];
+}
+
+void oracle_ce_fwd(const void* x, int64_t ld, const int64_t* labels, int64_t rows,
+                   int64_t cols, int64_t ignore, int dtype, float* rmax, float* rlse,
+                   float* loss) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    float m = -INFINITY;
+    for (int64_t j = 0; j < cols; ++j) {
+      const float v = load_logit(x, r * ld + j, dtype);
+      if (v > m || isnan(v)) m = v;
+    }
+    double acc = 0.0;
+    for (int64_t j = 0; j < cols; ++j) acc += exp((double)load_logit(x, r * ld + j, dtype) - (double)m);
+    const float lse = (float)log(acc);
+    rmax[r] = m;
+    rlse[r] = lse;
+    const int64_t t = labels[r];
+    if (t == ignore) {
+      loss[r] = 0.0f;
+    } else if (t < 0 || t >= cols) {
+      loss[r] = NAN;
+    } else {
+      const float xt = load_logit(x, r * ld + t, dtype);
+      loss[r] = -round_to((xt - m) - lse, dtype);
+    }
+  }
+}
+
+void oracle_ce_bwd(const void* x, int64_t ld, const int64_t* labels, const float* rmax,
+                   const float* rlse, float grad, int64_t rows, int64_t cols, int64_t ignore,
+                   int dtype, void* dx) {
+  const float neg = round_to(-grad, dtype);
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t t = labels[r];
+    const int bad = t != ignore && (t < 0 || t >= cols);
+    for (int64_t j = 0; j < cols; ++j) {
+      float d;
+      if (t == ignore) {
+        d = 0.0f;
+      } else if (bad) {
+        d = NAN;
+      } else {
+        const float logp = round_to((load_logit(x, r * ld + j, dtype) - rmax[r]) - rlse[r], dtype);
+        d = (j == t ? neg : 0.0f) - expf(logp) * neg;
+      }
+      if (dtype == F16) ((uint16_t*)dx)[r * ld + j] = oracle_f32_to_f16(d);
+      else ((float*)dx)[r * ld + j] = d;
+    }
+  }
 }

@@ -49,6 +49,8 @@ SIGNATURES = {
     "rv_residual_axpy": (_I, [_P, _P, _P, _I, _I64, _I, _I, _P]),
     "rv_add_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_cast_f32_f16": (_I, [_P, _P, _I64, _P]),
+    "rv_ce_fwd": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "rv_ce_bwd": (_I, [_P, _I, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_up_swiglu": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "rv_mlp_down": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_dgate": (_I, [_P, _P, _P, _I64, _I64, _I64, _P, _P]),
@@ -264,6 +266,34 @@ def _residual_axpy(x: torch.Tensor, f: torch.Tensor, sign: int):
     return out
 
 
+def _ce_fwd(logits: torch.Tensor, labels: torch.Tensor, ignore_index: int):
+    rows, cols = logits.shape
+    rmax, rlse, loss = (torch.empty(rows, device=logits.device, dtype=torch.float32)
+                        for _ in range(3))
+    if rows:
+        with _DeviceGuard(logits):
+            _check(library().rv_ce_fwd(logits.data_ptr(), _dtype_code(logits), logits.stride(0),
+                                       labels.data_ptr(), rows, cols, ignore_index,
+                                       rmax.data_ptr(), rlse.data_ptr(), loss.data_ptr(),
+                                       _stream(logits)),
+                   "rv_ce_fwd")
+    return rmax, rlse, loss
+
+
+def _ce_bwd(logits: torch.Tensor, labels: torch.Tensor, rmax: torch.Tensor, rlse: torch.Tensor,
+            grad: torch.Tensor, ignore_index: int):
+    rows, cols = logits.shape
+    dx = torch.empty_like(logits)
+    if rows:
+        with _DeviceGuard(logits):
+            _check(library().rv_ce_bwd(logits.data_ptr(), _dtype_code(logits), logits.stride(0),
+                                       labels.data_ptr(), rmax.data_ptr(), rlse.data_ptr(),
+                                       grad.data_ptr(), rows, cols, ignore_index, dx.data_ptr(),
+                                       _stream(logits)),
+                   "rv_ce_bwd")
+    return dx
+
+
 # ---------------------------------------------------------------------------
 # torch.library registration
 # ---------------------------------------------------------------------------
@@ -282,6 +312,10 @@ _SCHEMAS = {
     "midpoint_update_bwd": ("midpoint_update_bwd(Tensor dout, float scale, int sign, ScalarType force_dtype) -> Tensor",
                             _midpoint_update_bwd),
     "residual_axpy": ("residual_axpy(Tensor x, Tensor f, int sign) -> Tensor", _residual_axpy),
+    "ce_fwd": ("ce_fwd(Tensor logits, Tensor labels, int ignore_index) -> (Tensor, Tensor, Tensor)",
+               _ce_fwd),
+    "ce_bwd": ("ce_bwd(Tensor logits, Tensor labels, Tensor rmax, Tensor rlse, Tensor grad, "
+               "int ignore_index) -> Tensor", _ce_bwd),
 }
 for _name, (_schema, _impl) in _SCHEMAS.items():
     _library.define(_schema)
@@ -331,6 +365,17 @@ def _(dout, scale, sign, force_dtype):
 @torch.library.register_fake(f"{NAMESPACE}::residual_axpy")
 def _(x, f, sign):
     return torch.empty_like(x)
+
+
+@torch.library.register_fake(f"{NAMESPACE}::ce_fwd")
+def _(logits, labels, ignore_index):
+    rows = logits.shape[0]
+    return tuple(logits.new_empty(rows, dtype=torch.float32) for _ in range(3))
+
+
+@torch.library.register_fake(f"{NAMESPACE}::ce_bwd")
+def _(logits, labels, rmax, rlse, grad, ignore_index):
+    return torch.empty_like(logits)
 
 
 ops = getattr(torch.ops, NAMESPACE)

@@ -1,6 +1,15 @@
-"""Fused SwiGLU on gfx950, behind the reference's operator surface.
+"""Fused cross-entropy and SwiGLU on gfx950, behind the reference's operator surface.
 
-Mirrors ``FusedSwiGLU`` / ``enable_swiglu`` of src/reversibility/kernels.py:113-138:
+``TiledCrossEntropy`` / ``cross_entropy_sum`` mirror src/reversibility/kernels.py:56-85:
+``apply(logits, labels)`` takes contiguous ``[tokens, vocab]`` fp16/fp32 logits
+and int64 labels on the same device and returns the summed loss (fp32); rows
+labelled -100 contribute nothing.  It keeps the reference's Half-logsoftmax ->
+fp32 NLL policy: the log-probability at the target is rounded to the logits
+dtype before it is negated and summed, and the backward rounds the
+log-probability again before the exponential.  One HIP kernel reads each row
+once per pass (rv_ce_fwd / rv_ce_bwd).
+
+``FusedSwiGLU`` / ``enable_swiglu`` mirror src/reversibility/kernels.py:113-138:
 ``apply(up)`` takes the packed up-projection ``[..., 2W]`` (gate = first W
 columns, value = last W), returns ``[..., W]`` in the input dtype, and its
 backward returns the packed gradient.  Same ValueError contract (contiguous
@@ -16,6 +25,39 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from ._hip import ops
+
+
+IGNORE_INDEX = -100
+
+
+class TiledCrossEntropy(torch.autograd.Function):
+    """Summed cross-entropy over vocabulary rows (kernels.py:56-80)."""
+
+    @staticmethod
+    def forward(ctx, logits, labels):
+        if logits.device.type != "cuda" or logits.dtype not in (torch.float16, torch.float32):
+            raise ValueError("Fused CE requires CUDA (ROCm device) FP16/FP32 logits; "
+                             "no silent fallback")
+        if (logits.ndim != 2 or not logits.is_contiguous() or labels.device != logits.device
+                or labels.dtype != torch.int64 or labels.numel() != logits.shape[0]):
+            raise ValueError("Contiguous [tokens,vocab] logits and matching CUDA int64 labels "
+                             "required")
+        labels = labels.contiguous()
+        row_max, row_lse, losses = ops.ce_fwd(logits, labels, IGNORE_INDEX)
+        ctx.save_for_backward(logits, labels, row_max, row_lse)
+        return losses.sum()
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, gradient):
+        logits, labels, row_max, row_lse = ctx.saved_tensors
+        grad = gradient.detach().to(torch.float32).reshape(1).contiguous()
+        return ops.ce_bwd(logits, labels, row_max, row_lse, grad, IGNORE_INDEX), None
+
+
+def cross_entropy_sum(logits, labels):
+    """Sum of per-token cross-entropy losses (kernels.py:83-84)."""
+    return TiledCrossEntropy.apply(logits, labels)
 
 
 def _validate(up: torch.Tensor) -> None:

@@ -120,9 +120,15 @@ def chunked_backward(model, ids, labels, denominator, chunk_tokens, scaler=None,
 
 
 def _chunk_loss(logits, targets, loss_backend):
+    """Summed chunk loss.  ``"torch"`` is eager F.cross_entropy; ``"triton"``
+    (the reference's name for its fused loss, optimized.py:91-93) and
+    ``"hip"`` select the fused HIP cross-entropy."""
     if loss_backend == "torch":
         return F.cross_entropy(logits, targets, ignore_index=-100, reduction="sum")
-    raise ValueError(f"Unknown or unavailable loss backend {loss_backend!r}")
+    if loss_backend in ("triton", "hip"):
+        from .kernels import cross_entropy_sum
+        return cross_entropy_sum(logits, targets)
+    raise ValueError("Unknown loss backend")
 
 
 def cpu_snapshot(value):
