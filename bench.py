@@ -26,10 +26,17 @@ Also reported, on the same line:
                 (profiles/traffic.json), if recorded.
   kernels       the same per-kernel timing for every kernel of the step
                 (rms_bwd includes its small dw-reduce launch).
+  mlp_block     configs[2]: RMSNorm + tiled SwiGLU MLP block fwd+bwd, GEMM
+                TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak.
+  mlp_gemms     each MFMA MLP GEMM entry point alone at one 8192-token tile
+                of configs[2] and of configs[4], TFLOP/s and peak fraction.
   train_step    configs[3]: midpoint-reversible 7-layer decoder step
                 (B=33, T=512, fp16 autocast, GradScaler, clip 1.0, AdamW)
-                through install_v3(split core, 8192-token MLP tiles, fused
-                SwiGLU + RMSNorm), in tokens/s.
+                on the reference's v3 probe path (install_v3 split core,
+                8192-token MLP tiles, fused SwiGLU + RMSNorm, cached head with
+                the fused cross-entropy), in tokens/s.
+  train_step_c5 configs[4]: the 12-layer Hamiltonian-Euler d1024 step on
+                the same kernels (reconstruction-stack core), tokens/s.
   cpu_baseline  the CPU oracle (oracle/kernels_ref.c, OpenMP) on the host's
                 cores: the same RMSNorm + SwiGLU step, in GB/s.
 
@@ -76,6 +83,8 @@ def parse_args():
                    help="bounded CPU-baseline sample length (0 disables)")
     p.add_argument("--kernels-only", action="store_true",
                    help="only the kernel loop (used under rocprofv3)")
+    p.add_argument("--mlp-only", action="store_true",
+                   help="only the MLP block and MLP GEMM measurements (used under rocprofv3)")
     return p.parse_args()
 
 
@@ -297,6 +306,90 @@ def train_step_bench(dev, steps: int, warmup: int, name: str = "c4"):
             "data": "synthetic uniform token ids (seed 1337)"}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16
+
+
+def _event_time_us(fn, reps: int, warmup: int = 3) -> float:
+    """Average duration of fn's launches (HIP events on the current stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps * 1e3
+
+
+def mlp_gemm_bench(dev, reps: int = 20):
+    """MFMA MLP GEMMs alone, per entry point, at one token tile of configs[2]
+    (8192 x d256 x f1024) and of configs[4] (8192 x d1024 x f4096): TFLOP/s
+    of the algorithmic contraction and the fraction of the dense fp16 peak.
+    Epilogues (SwiGLU and its backward, fp16 rounding, accumulation) are
+    inside the measured kernels."""
+    import torch
+    from reversability_amd import mlp
+    out = {}
+    for rows, d, f in ((8192, 256, 1024), (8192, 1024, 4096)):
+        g = torch.Generator(device=dev).manual_seed(1337)
+        x16 = torch.randn(rows, d, device=dev, generator=g).half()
+        up16 = (0.02 * torch.randn(2 * f, d, device=dev, generator=g)).half()
+        down16 = (0.02 * torch.randn(d, f, device=dev, generator=g)).half()
+        dy = torch.randn(rows, d, device=dev, generator=g).half()
+        o, u = mlp.up_swiglu(x16, up16, keep_u=True)
+        du = mlp.dgate(dy, down16, u)
+        y = torch.empty(rows, d, device=dev, dtype=torch.float16)
+        dx = torch.empty(rows, d, device=dev)
+        ddown, dup = torch.empty(d, f, device=dev), torch.empty(2 * f, d, device=dev)
+        cases = {
+            "up_swiglu": (lambda: mlp.up_swiglu(x16, up16), 2 * rows * 2 * f * d),
+            "down": (lambda: mlp.down(o, down16, y), 2 * rows * d * f),
+            "dgate_swiglu_bwd": (lambda: mlp.dgate(dy, down16, u), 2 * rows * f * d),
+            "dx": (lambda: mlp.dx(du, up16, dx), 2 * rows * 2 * f * d),
+            "wgrad": (lambda: mlp.wgrad(dy, o, du, x16, ddown, dup, True),
+                      2 * rows * d * f + 2 * rows * 2 * f * d),
+        }
+        line = {}
+        for name, (fn, flops) in cases.items():
+            us = _event_time_us(fn, reps)
+            tf = flops / us / 1e6
+            line[name] = {"us": round(us, 1), "TFLOPs": round(tf, 1),
+                          "frac": round(tf / MFMA_PEAK_TFLOPS, 4)}
+        out[f"tile{rows}_d{d}_f{f}"] = line
+    return out
+
+
+def mlp_block_bench(dev, steps: int = 20):
+    """RMSNorm + token-tiled SwiGLU MLP block (TiledMLP, 8192-token
+    tiles: rows [0, 8192) and [8192, 14848)) under fp16 autocast with an fp32
+    residual input, forward + backward against a random fp32 upstream
+    gradient.  Algorithmic GEMM work fwd+bwd: 70,061,654,016 flop."""
+    import torch
+    from reversability_amd.kernels_v3 import FusedRMSNorm
+    from reversability_amd.optimized_v3 import TiledMLP
+    g = torch.Generator().manual_seed(1337)
+    x = torch.randn(29, 512, 256, generator=g).to(dev).requires_grad_(True)
+    up = (0.02 * torch.randn(2048, 256, generator=g)).to(dev).requires_grad_(True)
+    down = (0.02 / 14 ** 0.5 * torch.randn(256, 1024, generator=g)).to(dev).requires_grad_(True)
+    w = torch.ones(256, device=dev, requires_grad=True)
+    gy = torch.randn(29, 512, 256, generator=g).to(dev)
+    eps = float(torch.finfo(torch.float32).eps)
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.float16):
+            out = TiledMLP.apply(FusedRMSNorm.apply(x, w, eps), up, down, 8192, True)
+        torch.autograd.backward(out, gy)
+
+    us = _event_time_us(step, steps)
+    flops = 70_061_654_016
+    return {"workload": "configs[2] tiled MLP block 29x512 d256 f1024 tile 8192, fp16 autocast",
+            "ms_per_step": round(us / 1e3, 4), "gemm_TFLOPs": round(flops / us / 1e6, 1),
+            "frac_of_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4),
+            "algorithmic_flop": flops}
+
+
 def cpu_baseline(seconds: float):
     """Oracle (C, OpenMP) on this host's cores: the same RMSNorm+SwiGLU step."""
     import numpy as np
@@ -357,6 +450,10 @@ def main() -> int:
     if args.kernels_only:
         kernel_loop_only(dev, args.steps, args.warmup)
         return 0
+    if args.mlp_only:
+        print(json.dumps({"mlp_block": mlp_block_bench(dev), "mlp_gemms": mlp_gemm_bench(dev)}),
+              flush=True)
+        return 0
     ms_step_s, per_kernel = time_kernels(dev, args.steps, args.warmup)
     value = STEP_BYTES / ms_step_s / 1e9
     bytes_by = {"rms_fwd": RMS_FWD_BYTES, "rms_bwd": RMS_BWD_BYTES,
@@ -391,7 +488,10 @@ def main() -> int:
         "kernels": kernels,
     }
     if not args.no_train_step:
+        line["mlp_block"] = mlp_block_bench(dev)
+        line["mlp_gemms"] = mlp_gemm_bench(dev)
         line["train_step"] = train_step_bench(dev, args.train_steps, args.train_warmup)
+        line["train_step_c5"] = train_step_bench(dev, 3, 2, "c5")
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
