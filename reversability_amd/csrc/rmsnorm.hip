@@ -44,7 +44,10 @@ using rv::wave_sum;
 
 
 constexpr int kFwdWaves = 4;                 // waves per block, forward
-constexpr int kBwdWaves = RV_RMS_BWD_WAVES;  // waves per block, backward
+constexpr int kBwdWaves = RV_RMS_BWD_WAVES;  // waves per block, backward (width <= 512)
+// Waves per backward block by vector count per lane (width <= 256 * VEC):
+// 2 rows x (x, dy) x VEC float4 per register tile, two tiles in flight.
+constexpr int bwd_waves(int vec) { return vec <= 2 ? kBwdWaves : (vec == 4 ? 8 : 4); }
 constexpr int kMaxVec = 16;      // float4 per lane => width <= 4096
 constexpr int kMaxEpl = 64;      // scalar path: elements per lane <= 64
 
@@ -281,8 +284,10 @@ __device__ __forceinline__ void bwd_finish(BwdTile<VEC>& t, const float4 (&wv)[V
   }
 }
 
-template <int VEC>
-__global__ __launch_bounds__(kBwdWaves * 64)
+// WAVES per block: wide rows keep fewer waves so that their two-row
+// ping-pong tiles stay in registers (no scratch).
+template <int VEC, int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
 void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
                  const float* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
@@ -302,7 +307,7 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
   }
 
   const int64_t first = start + 2 * wave;
-  const int64_t stride = 2 * kBwdWaves;
+  const int64_t stride = 2 * WAVES;
   if (first < end) {  // wave-uniform
     const int64_t iters = (end - 1 - first) / stride + 1;
     int64_t row0 = first;
@@ -322,16 +327,16 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
   // Combine the waves' column partials in wave order, at most 4 float4 per
   // lane per pass.
   constexpr int kPass = VEC < 4 ? VEC : 4;
-  __shared__ float4 red[kBwdWaves][kPass * 64];
+  __shared__ float4 red[WAVES][kPass * 64];
 #pragma unroll
   for (int v0 = 0; v0 < VEC; v0 += kPass) {
 #pragma unroll
     for (int v = 0; v < kPass; ++v) red[wave][v * 64 + lane] = acc[v0 + v];
     __syncthreads();
-    for (int s = threadIdx.x; s < kPass * 64; s += kBwdWaves * 64) {
+    for (int s = threadIdx.x; s < kPass * 64; s += WAVES * 64) {
       float4 t = red[0][s];
 #pragma unroll
-      for (int k = 1; k < kBwdWaves; ++k) {
+      for (int k = 1; k < WAVES; ++k) {
         t.x = t.x + red[k][s].x;
         t.y = t.y + red[k][s].y;
         t.z = t.z + red[k][s].z;
@@ -569,9 +574,9 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
                    rv_host::aligned16(dx);
   if (vec) {
     const int vecs = (iw + 255) / 256;
-#define RV_BWD_VEC(V)                                                       \
-  hipLaunchKernelGGL((rms_bwd_vec<V>), grid, block, 0, s, x, w, dy, rstd, dx, \
-                     partial, rows, iw, p.rows_per_block)
+#define RV_BWD_VEC(V)                                                             \
+  hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V)>), grid, dim3(bwd_waves(V) * 64), 0, s, x, \
+                     w, dy, rstd, dx, partial, rows, iw, p.rows_per_block)
     if (vecs <= 1) RV_BWD_VEC(1);
     else if (vecs <= 2) RV_BWD_VEC(2);
     else if (vecs <= 4) RV_BWD_VEC(4);
