@@ -244,7 +244,8 @@ def make_train_step(dev, name: str):
     """One full training update of a TRAIN_CONFIGS entry, on the reference's
     v3 probe path (scripts/benchmark_midpoint_v3.py:78-83 over
     scripts/benchmark_optimized.py:54-82): install_v3 (split core for the
-    midpoint config, 8192-token tiled MLP, fused SwiGLU and RMSNorm), then
+    midpoint config, 8192-token tiled MLP, fused SwiGLU and RMSNorm), the
+    attention projections on the MFMA kernels (enable_linear), then
     cached_head_backward -- fp16 autocast core forward, the tied head and the
     fused cross-entropy in HEAD_CHUNK-token chunks, sum loss / valid targets, one
     core backward -- then GradScaler unscale, clip 1.0 and AdamW (0.9, 0.95),
@@ -253,6 +254,7 @@ def make_train_step(dev, name: str):
     import numpy as np
     import torch
     from reversability_amd import build_model
+    from reversability_amd.linear import enable_linear
     from reversability_amd.optimized_v3 import cached_head_backward, install_v3
 
     cfg = TRAIN_CONFIGS[name]
@@ -262,6 +264,7 @@ def make_train_step(dev, name: str):
     model = build_model({"model": cfg["model"], "method": cfg["method"],
                          "step_size": cfg["step_size"]}).to(dev)
     install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    enable_linear(model)
     opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
     scaler = torch.amp.GradScaler("cuda")
     # one uint16 stream of B*T+1 uniform ids; x = stream[:-1], y = stream[1:]

@@ -208,6 +208,33 @@ int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x,
                  int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Bias-free linear layers under fp16 autocast on the same MFMA kernels: the
+ * attention's qkv and output projections (src/reversibility/model.py:26-45,
+ * nn.Linear under torch.autocast, as called from midpoint_force /
+ * forward_pair, src/reversibility/reversible.py:16-25).  x and dy fp16,
+ * w fp16 [out, in] (cast once per call with rv_cast_f32_f16); in and out
+ * multiples of 128.
+ */
+
+/* y[rows, out] = fp16(x W^T), x with row stride ldx. */
+int rv_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t rows,
+                  int64_t in, int64_t out, void* y, void* stream);
+
+/* dx[rows, in] = fp16(dy W), widened to fp32 when dx_dtype == RV_F32 (the
+ * gradient autocast returns for an fp32 input). */
+int rv_linear_dx(const void* dy, const void* w, int64_t rows, int64_t in,
+                 int64_t out, void* dx, int dx_dtype, void* stream);
+
+/* Scratch bytes rv_linear_dw needs (split-K partial sums; may be 0). */
+int64_t rv_linear_dw_workspace_bytes(int64_t rows, int64_t in, int64_t out);
+
+/* dw[out, in] (+)= fp32(fp16(dy^T x)), reduced over the rows in a fixed order
+ * (the fp32 master-weight gradient autocast produces). */
+int rv_linear_dw(const void* dy, const void* x, int64_t ldx, int64_t rows,
+                 int64_t in, int64_t out, float* dw, int accumulate,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Cross-entropy over vocabulary rows (the tied LM head's loss).
  * logits [rows, ld] fp16 (RV_F16) or fp32 (RV_F32), first cols columns used;
  * labels int64 [rows]; rows whose label equals ignore_index contribute 0.

@@ -537,6 +537,11 @@ template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF32OfF16>(G
 template __global__ void gemm_kernel<64, 128, true, true, Epi::AccF32OfF16>(GemmArgs);
 template __global__ void gemm_kernel<64, 128, true, true, Epi::PartialF32>(GemmArgs);
 
+template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, true, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, true, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF16>(GemmArgs);
+
 // acc[i] (+)= fp32(fp16(sum_s part[s][i])), splits summed in order.  This is
 // autocast's weight gradient: the fp16 GEMM result, cast to the fp32 weight
 // and added to the running per-tile sum.  n % 4 == 0.
@@ -777,6 +782,63 @@ int rv_mlp_dx(const void* du, const void* w_up, int64_t rows, int64_t d, int64_t
   a.m = rows; a.n = d; a.k = 2 * f;
   a.c = dx; a.ldc = d;
   return run_act<false, true, Epi::StoreF32OfF16>(a, d, (hipStream_t)stream);
+}
+
+int rv_linear_fwd(const void* x, int64_t ldx, const void* w, int64_t rows, int64_t in,
+                  int64_t out, void* y, void* stream) {
+  if (!x || !w || !y) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || in <= 0 || out <= 0 || ldx < in) return RV_ERR_BAD_SIZE;
+  if (in % 128 || out % 128 || ldx % 8) return RV_ERR_UNSUPPORTED;
+  if (!ok16(x) || !ok16(w) || !ok16(y)) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * ldx) || !fits32(out * in)) return RV_ERR_UNSUPPORTED;
+  GemmArgs a{};
+  a.a = static_cast<const __half*>(x); a.lda = ldx; a.a_bytes = rows * ldx * 2;
+  a.b = static_cast<const __half*>(w); a.ldb = in; a.b_bytes = out * in * 2;
+  a.m = rows; a.n = out; a.k = in;
+  a.c = y; a.ldc = out;
+  return run_act<false, false, Epi::StoreF16>(a, out, (hipStream_t)stream);
+}
+
+int rv_linear_dx(const void* dy, const void* w, int64_t rows, int64_t in, int64_t out, void* dx,
+                 int dx_dtype, void* stream) {
+  if (!dy || !w || !dx) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || in <= 0 || out <= 0) return RV_ERR_BAD_SIZE;
+  if (in % 128 || out % 128) return RV_ERR_UNSUPPORTED;
+  if (dx_dtype != RV_F16 && dx_dtype != RV_F32) return RV_ERR_UNSUPPORTED;
+  if (!ok16(dy) || !ok16(w) || !ok16(dx)) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * out) || !fits32(out * in)) return RV_ERR_UNSUPPORTED;
+  GemmArgs a{};
+  a.a = static_cast<const __half*>(dy); a.lda = out; a.a_bytes = rows * out * 2;
+  a.b = static_cast<const __half*>(w); a.ldb = in;  // B(i, o) = W[o][i]: RC
+  a.b_bytes = out * in * 2;
+  a.m = rows; a.n = in; a.k = out;
+  a.c = dx; a.ldc = in;
+  const hipStream_t s = (hipStream_t)stream;
+  return dx_dtype == RV_F16 ? run_act<false, true, Epi::StoreF16>(a, in, s)
+                            : run_act<false, true, Epi::StoreF32OfF16>(a, in, s);
+}
+
+int64_t rv_linear_dw_workspace_bytes(int64_t rows, int64_t in, int64_t out) {
+  if (rows <= 0 || in <= 0 || out <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
+  const int64_t b = wgrad_part_bytes(rows, out, in);
+  return b < 0 ? -(int64_t)RV_ERR_UNSUPPORTED : b;
+}
+
+int rv_linear_dw(const void* dy, const void* x, int64_t ldx, int64_t rows, int64_t in,
+                 int64_t out, float* dw, int accumulate, void* workspace, int64_t workspace_bytes,
+                 void* stream) {
+  if (!dy || !x || !dw) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || in <= 0 || out <= 0 || ldx < in) return RV_ERR_BAD_SIZE;
+  if (in % 128 || out % 128 || ldx % 8) return RV_ERR_UNSUPPORTED;
+  if (!ok16(dy) || !ok16(x) || !ok16(dw)) return RV_ERR_UNSUPPORTED;
+  if (!fits32(rows * out) || !fits32(rows * ldx)) return RV_ERR_UNSUPPORTED;
+  const int64_t need = rv_linear_dw_workspace_bytes(rows, in, out);
+  if (need < 0) return (int)-need;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !ok16(workspace)))
+    return RV_ERR_WORKSPACE;
+  // dW[out][in] = sum_m dy[m][o] x[m][i]
+  return run_wgrad(static_cast<const __half*>(dy), out, static_cast<const __half*>(x), ldx, rows,
+                   out, in, dw, accumulate, static_cast<float*>(workspace), (hipStream_t)stream);
 }
 
 int64_t rv_mlp_wgrad_workspace_bytes(int64_t rows, int64_t d, int64_t f) {

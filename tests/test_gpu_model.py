@@ -24,7 +24,8 @@ import torch.nn.functional as F
 from reconstruction_gate import TOLERANCES, check_case
 from reversability_amd import build_model
 from reversability_amd.kernels_v3 import FusedRMSNorm
-from reversability_amd.optimized_v3 import TiledMLP, install_v3
+from reversability_amd.linear import enable_linear
+from reversability_amd.optimized_v3 import TiledMLP, cached_head_backward, install_v3
 from reversability_amd.reversible import forward_pair, inverse_pair
 
 pytestmark = pytest.mark.gpu
@@ -247,6 +248,36 @@ def test_full_midpoint_step_matches_autograd(cuda_device, core):
     inc = sum((p.detach() - before[n]).double().square().sum().item()
               for n, p in reference.named_parameters())
     assert math.sqrt(diff / inc) <= 0.05
+
+
+def test_bench_path_step_matches_autograd(cuda_device):
+    """The measured training step's path -- split core, tiled MLP, fused SwiGLU
+    and RMSNorm, MFMA attention projections, cached head with the fused
+    cross-entropy over the whole batch -- against eager autograd of the same
+    model with F.cross_entropy (loss within 2e-3, every parameter gradient
+    within relative L2 2e-2)."""
+    torch.manual_seed(1337)
+    reference = build_model(C4).to(cuda_device)
+    candidate = copy.deepcopy(reference)
+    reference.backward_mode = "autograd"
+    install_v3(candidate, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    enable_linear(candidate)
+    x, y = _c4_batch(cuda_device)
+    loss_r, grads_r = _step_grads(reference, x, y)
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 10)
+    candidate.zero_grad(set_to_none=True)
+    total = cached_head_backward(candidate, x, y, y.numel(), y.numel(), scaler, "fp16", False,
+                                 "triton")
+    inv = 1.0 / scaler.get_scale()
+    loss_c = total / y.numel()
+    print(f"\n[c4 bench path] loss {loss_c.item():.6f} eager {loss_r.item():.6f}", flush=True)
+    assert abs(loss_c.item() - loss_r.item()) <= 2e-3 * abs(loss_r.item())
+    worst = 0.0
+    for name, p in candidate.named_parameters():
+        r = rel_l2(p.grad * inv, grads_r[name])
+        worst = max(worst, r)
+        assert r < 2e-2, (name, r)
+    print(f"[c4 bench path] worst parameter-gradient relative L2 {worst:.3e}", flush=True)
 
 
 def test_full_step_reconstruction_error(cuda_device):
