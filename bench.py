@@ -249,12 +249,14 @@ def make_train_step(dev, name: str):
     cached_head_backward -- fp16 autocast core forward, the tied head and the
     fused cross-entropy in HEAD_CHUNK-token chunks, sum loss / valid targets, one
     core backward -- then GradScaler unscale, clip 1.0 and AdamW (0.9, 0.95),
-    wd 0.1.  Returns (step function returning the summed loss, targets per
-    step, config)."""
+    wd 0.1 (FusedAdamW: one multi-tensor HIP pass, no host synchronisation).
+    Returns (step function returning the summed loss, targets per step,
+    config)."""
     import numpy as np
     import torch
     from reversability_amd import build_model
     from reversability_amd.linear import enable_linear
+    from reversability_amd.optim import FusedAdamW
     from reversability_amd.optimized_v3 import cached_head_backward, install_v3
 
     cfg = TRAIN_CONFIGS[name]
@@ -265,7 +267,7 @@ def make_train_step(dev, name: str):
                          "step_size": cfg["step_size"]}).to(dev)
     install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True)
     enable_linear(model)
-    opt = torch.optim.AdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    opt = FusedAdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
     scaler = torch.amp.GradScaler("cuda")
     # one uint16 stream of B*T+1 uniform ids; x = stream[:-1], y = stream[1:]
     stream = np.random.default_rng(1337).integers(0, vocab, batch * length + 1).astype(np.uint16)

@@ -235,6 +235,30 @@ int rv_linear_dw(const void* dy, const void* x, int64_t ldx, int64_t rows,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * AdamW (decoupled weight decay) over fp32 parameters, torch.optim.AdamW's
+ * arithmetic and operation order, as the training step drives it through
+ * torch.amp.GradScaler (scripts/benchmark_optimized.py:38-40, 66-80;
+ * scripts/train_baseline.py:270-284).  The step count is a device fp32 per
+ * parameter group.
+ */
+
+/* Largest tensor count one rv_adamw_step call accepts. */
+int rv_adamw_max_tensors(void);
+
+/* *step += 1 unless found_inf is given and *found_inf != 0. */
+int rv_adamw_advance(float* step, const float* found_inf, void* stream);
+
+/* One update of count tensors (arrays of device pointers and sizes in host
+ * memory): p, m, v updated in place from g (times *inv_scale if given), with
+ * the bias corrections of the (already advanced) *step; nothing changes when
+ * found_inf is given and *found_inf != 0. */
+int rv_adamw_step(int count, float* const* params, const float* const* grads,
+                  float* const* exp_avg, float* const* exp_avg_sq,
+                  const int64_t* numel, double lr, double beta1, double beta2,
+                  double eps, double weight_decay, const float* step,
+                  const float* found_inf, const float* inv_scale, void* stream);
+
+/* ------------------------------------------------------------------------
  * Cross-entropy over vocabulary rows (the tied LM head's loss).
  * logits [rows, ld] fp16 (RV_F16) or fp32 (RV_F32), first cols columns used;
  * labels int64 [rows]; rows whose label equals ignore_index contribute 0.

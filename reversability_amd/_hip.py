@@ -53,6 +53,9 @@ SIGNATURES = {
     "rv_linear_dx": (_I, [_P, _P, _I64, _I64, _I64, _P, _I, _P]),
     "rv_linear_dw_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "rv_linear_dw": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P, _I, _P, _I64, _P]),
+    "rv_adamw_max_tensors": (_I, []),
+    "rv_adamw_advance": (_I, [_P, _P, _P]),
+    "rv_adamw_step": (_I, [_I, _P, _P, _P, _P, _P, _D, _D, _D, _D, _D, _P, _P, _P, _P]),
     "rv_ce_fwd": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "rv_ce_bwd": (_I, [_P, _I, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_up_swiglu": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
