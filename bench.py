@@ -245,7 +245,10 @@ def make_train_step(dev, name: str):
     v3 probe path (scripts/benchmark_midpoint_v3.py:78-83 over
     scripts/benchmark_optimized.py:54-82): install_v3 (split core for the
     midpoint config, 8192-token tiled MLP, fused SwiGLU and RMSNorm), the
-    attention projections on the MFMA kernels (enable_linear), then
+    attention projections on the MFMA kernels (enable_linear), the fused token +
+    position embedding adding its token gradient into the tied weight's
+    gradient (enable_embedding), the batch cut from a uint16 token stream
+    resident in HBM (batch_at over DeviceTokens), then
     cached_head_backward -- fp16 autocast core forward, the tied head and the
     fused cross-entropy in HEAD_CHUNK-token chunks, sum loss / valid targets, one
     core backward -- then GradScaler unscale, clip 1.0 and AdamW (0.9, 0.95),
@@ -255,6 +258,8 @@ def make_train_step(dev, name: str):
     import numpy as np
     import torch
     from reversability_amd import build_model
+    from reversability_amd.data import DeviceTokens, batch_at
+    from reversability_amd.embedding import enable_embedding
     from reversability_amd.linear import enable_linear
     from reversability_amd.optim import FusedAdamW
     from reversability_amd.optimized_v3 import cached_head_backward, install_v3
@@ -267,15 +272,17 @@ def make_train_step(dev, name: str):
                          "step_size": cfg["step_size"]}).to(dev)
     install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True)
     enable_linear(model)
+    enable_embedding(model, into_grad=True)
     opt = FusedAdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
     scaler = torch.amp.GradScaler("cuda")
-    # one uint16 stream of B*T+1 uniform ids; x = stream[:-1], y = stream[1:]
+    # one uint16 stream of B*T+1 uniform ids, resident in HBM; each step cuts
+    # x = stream[:-1], y = stream[1:] from it (batch_at)
     stream = np.random.default_rng(1337).integers(0, vocab, batch * length + 1).astype(np.uint16)
-    x = torch.from_numpy(stream[:-1].astype(np.int64).reshape(batch, length)).to(dev)
-    y = torch.from_numpy(stream[1:].astype(np.int64).reshape(batch, length)).to(dev)
+    tokens = DeviceTokens(stream, dev)
     targets = batch * length
 
     def step():
+        x, y, _ = batch_at(tokens, 0, batch, length, targets)
         opt.zero_grad(set_to_none=True)
         loss = cached_head_backward(model, x, y, targets, HEAD_CHUNK or targets, scaler, "fp16",
                                     False, "triton")

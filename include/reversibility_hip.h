@@ -282,6 +282,39 @@ int rv_ce_bwd(const void* logits, int dtype, int64_t ld, const int64_t* labels,
               int64_t rows, int64_t cols, int64_t ignore_index, void* dlogits,
               void* stream);
 
+/* ------------------------------------------------------------------------
+ * Token pipeline and token + position embedding (the steps in front of the
+ * reversible stack).  Tables and activations fp32, d a multiple of 4, fp32
+ * pointers 16-byte aligned.
+ */
+
+/* batch_at (scripts/train_baseline.py:50-63) on a device window of count + 1
+ * uint16 tokens: x[i] = window[i], y[i] = window[i + 1] for i < count, then
+ * x = 0, y = -100 up to ceil(count / seq_len) * seq_len entries (int64). */
+int rv_batch_from_tokens(const uint16_t* window, int64_t count, int64_t seq_len,
+                         int64_t* x, int64_t* y, void* stream);
+
+/* out[b, t] = tok[ids[b, t]] + pos[t] (src/reversibility/reversible.py:105-106,
+ * the boundary p = q = embedding; model.py's token and position
+ * nn.Embedding).  An id outside [0, vocab) gives a NaN row. */
+int rv_embed_fwd(const int64_t* ids, int64_t batch, int64_t seq, const float* tok,
+                 int64_t vocab, const float* pos, int64_t max_seq, int64_t d,
+                 float* out, void* stream);
+
+/* Workspace bytes rv_embed_bwd needs for this many tokens (negative: -error). */
+int64_t rv_embed_bwd_workspace_bytes(int64_t tokens, int64_t vocab, int64_t d);
+
+/* The embedding's backward, deterministic: dtok[v] (+)= sum of dout rows
+ * whose id is v (nn.Embedding's weight gradient; rows of untouched ids are
+ * zeroed unless accumulating, ids outside [0, vocab) get nothing) and
+ * dpos[t] (+)= sum_b dout[b, t] (the position embedding's gradient through
+ * the broadcast add; rows seq <= t < max_seq zeroed unless accumulating).
+ * Either output may be NULL. */
+int rv_embed_bwd(const int64_t* ids, int64_t batch, int64_t seq, const float* dout,
+                 int64_t vocab, int64_t max_seq, int64_t d, float* dtok,
+                 int tok_accumulate, float* dpos, int pos_accumulate,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

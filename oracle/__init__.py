@@ -12,7 +12,10 @@ Contents
     :func:`swiglu_fwd`, :func:`swiglu_bwd` (src/reversibility/kernels.py:88-110),
     :func:`midpoint`, :func:`midpoint_bwd`, :func:`euler`
     (src/reversibility/reversible.py:16-32), :func:`ce_fwd`, :func:`ce_bwd`
-    (src/reversibility/kernels.py:14-77).
+    (src/reversibility/kernels.py:14-77), :func:`embed_fwd`, :func:`embed_bwd`
+    (src/reversibility/reversible.py:105-106 with model.py's two nn.Embedding).
+:func:`batch_at`
+    numpy restatement of scripts/train_baseline.py:50-63.
 ``model_ref.py``
     torch-CPU functional restatement of the decoder and both integrators
     (src/reversibility/model.py, reversible.py) for model-level checks.
@@ -29,6 +32,15 @@ How each function is pinned (tests/test_oracle.py):
         uniform-logits closed form log V, torch's eager fp16 log_softmax at
         the target (the reference's Half-logsoftmax policy), zero column sums
         of the gradient, ignore_index rows.
+    batch_at        -- the reference's own test vector
+        (tests/test_baseline.py:30-38), the shift identity x[1:] == y[:-1]
+        on its test stream (arange(4097) % 31, tests/test_optimized.py:89),
+        target counts of partial batches, StopIteration past the limit.
+    embed_fwd       -- numpy gather + broadcast add (library), bit for bit.
+    embed_bwd       -- np.add.at / numpy sum over the batch on small-integer
+        gradients (exact in any order), fp64 sums at fp32 tolerance, the
+        block order changing nothing for runs inside one block, ids outside
+        the vocabulary contributing nothing, accumulation.
     f16 conversion  -- all 65536 binary16 patterns round-trip; numpy's
         float16 cast on 2^20 random floats including subnormals/overflow.
 """
@@ -79,6 +91,9 @@ def lib() -> ctypes.CDLL:
             "oracle_f16_to_f32_array": (None, [P, P, I64]),
             "oracle_ce_fwd": (None, [P, I64, P, I64, I64, I64, I, P, P, P]),
             "oracle_ce_bwd": (None, [P, I64, P, P, P, F, I64, I64, I64, I, P]),
+            "oracle_embed_fwd": (None, [P, I64, I64, P, I64, P, I64, P]),
+            "oracle_embed_bwd_pos": (None, [P, I64, I64, I64, I64, P, I]),
+            "oracle_embed_bwd_tok": (None, [P, I64, P, I64, I64, I64, P, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -231,3 +246,57 @@ def ce_bwd(x: np.ndarray, labels: np.ndarray, rmax: np.ndarray, rlse: np.ndarray
     lib().oracle_ce_bwd(_ptr(x), cols, _ptr(labels), _ptr(rmax), _ptr(rlse), grad, rows, cols,
                         ignore_index, _code(x), _ptr(dx))
     return dx
+
+
+IGNORE_INDEX = -100
+EMBED_RUN_BLOCK = 16  # sorted entries per block in the device token-gradient reduction
+
+
+def batch_at(data: np.ndarray, cursor: int, batch_size: int, sequence_length: int,
+             target_limit: int):
+    """(x, y, count) int64 [sequences, sequence_length] from a uint16 token
+    stream (scripts/train_baseline.py:50-63): x = stream[cursor:cursor+count],
+    y shifted by one, padded with x = 0 and y = -100."""
+    count = min(batch_size * sequence_length, target_limit - cursor)
+    if count <= 0:
+        raise StopIteration
+    sequences = -(-count // sequence_length)
+    raw = np.asarray(data[cursor:cursor + count + 1], dtype=np.int64)
+    x = np.zeros(sequences * sequence_length, np.int64)
+    y = np.full(sequences * sequence_length, IGNORE_INDEX, np.int64)
+    x[:count] = raw[:-1]
+    y[:count] = raw[1:]
+    return x.reshape(sequences, sequence_length), y.reshape(sequences, sequence_length), count
+
+
+def embed_fwd(ids: np.ndarray, tok: np.ndarray, pos: np.ndarray) -> np.ndarray:
+    """tok[ids] + pos[:T] as float32 [B, T, d]; NaN rows for ids outside the table."""
+    ids = np.ascontiguousarray(ids, np.int64)
+    tok = np.ascontiguousarray(tok, np.float32)
+    pos = np.ascontiguousarray(pos, np.float32)
+    batch, seq = ids.shape
+    d = tok.shape[1]
+    out = np.empty((batch, seq, d), np.float32)
+    lib().oracle_embed_fwd(_ptr(ids), batch * seq, seq, _ptr(tok), tok.shape[0], _ptr(pos), d,
+                           _ptr(out))
+    return out
+
+
+def embed_bwd(ids: np.ndarray, dout: np.ndarray, vocab: int, max_seq: int, dtok=None, dpos=None,
+              block: int = EMBED_RUN_BLOCK):
+    """(dtok [vocab, d], dpos [max_seq, d]) float32.  Given dtok / dpos arrays
+    are accumulated into (in place); otherwise fresh ones are returned."""
+    ids = np.ascontiguousarray(ids, np.int64)
+    dout = np.ascontiguousarray(dout, np.float32)
+    batch, seq = ids.shape
+    d = dout.shape[-1]
+    tok_acc, pos_acc = dtok is not None, dpos is not None
+    if dtok is None:
+        dtok = np.empty((vocab, d), np.float32)
+    if dpos is None:
+        dpos = np.empty((max_seq, d), np.float32)
+    assert dtok.flags.c_contiguous and dpos.flags.c_contiguous
+    lib().oracle_embed_bwd_tok(_ptr(ids), batch * seq, _ptr(dout), vocab, d, block, _ptr(dtok),
+                               int(tok_acc))
+    lib().oracle_embed_bwd_pos(_ptr(dout), batch, seq, max_seq, d, _ptr(dpos), int(pos_acc))
+    return dtok, dpos

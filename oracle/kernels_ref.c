@@ -18,6 +18,12 @@
  *                        _ce_rows, TiledCrossEntropy.forward)
  *   oracle_ce_bwd        src/reversibility/kernels.py:48-60,69-77 (_ce_grad,
  *                        TiledCrossEntropy.backward)
+ *   oracle_embed_fwd     src/reversibility/reversible.py:105-106, model.py
+ *                        (token_embedding(ids) + position_embedding(arange(T)))
+ *   oracle_embed_bwd_pos the position table's gradient through the broadcast
+ *                        add: sum over the batch, in batch order
+ *   oracle_embed_bwd_tok nn.Embedding's weight gradient, summed per id in the
+ *                        fixed order of the device kernel (see below)
  *
  * RMSNorm sums are accumulated in double (a tighter reference than any fp32
  * summation order); outputs are rounded once to float.  SwiGLU uses float
@@ -356,4 +362,93 @@ void oracle_ce_bwd(const void* x, int64_t ld, const int64_t* labels, const float
       else ((float*)dx)[r * ld + j] = d;
     }
   }
+}
+
+/* ---- token + position embedding --------------------------------------- */
+
+/* out[i] = tok[ids[i]] + pos[i % seq] (one fp32 add per element); an id
+ * outside [0, vocab) gives a NaN row. */
+void oracle_embed_fwd(const int64_t* ids, int64_t n, int64_t seq, const float* tok,
+                      int64_t vocab, const float* pos, int64_t d, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t id = ids[i];
+    const float* pr = pos + (i % seq) * d;
+    float* o = out + i * d;
+    if (id < 0 || id >= vocab) {
+      for (int64_t c = 0; c < d; ++c) o[c] = NAN;
+      continue;
+    }
+    const float* tr = tok + id * d;
+    for (int64_t c = 0; c < d; ++c) o[c] = tr[c] + pr[c];
+  }
+}
+
+/* dpos[t] = (dpos[t] if accumulate else 0) + (((0 + dout[0, t]) + dout[1, t])
+ * + ...); rows seq <= t < max_seq are zeroed unless accumulating. */
+void oracle_embed_bwd_pos(const float* dout, int64_t batch, int64_t seq, int64_t max_seq,
+                          int64_t d, float* dpos, int accumulate) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < max_seq; ++t) {
+    float* dst = dpos + t * d;
+    if (t >= seq) {
+      if (!accumulate)
+        for (int64_t c = 0; c < d; ++c) dst[c] = 0.0f;
+      continue;
+    }
+    for (int64_t c = 0; c < d; ++c) {
+      float acc = 0.0f;
+      for (int64_t b = 0; b < batch; ++b) acc = acc + dout[(b * seq + t) * d + c];
+      dst[c] = accumulate ? dst[c] + acc : acc;
+    }
+  }
+}
+
+/* dtok[v] = (dtok[v] if accumulate else 0) + S_v, S_v the sum of the dout rows
+ * of the occurrences of v in this order: the occurrences, in ascending token
+ * index, are the run of v in the id-sorted token list; that list is cut into
+ * blocks of `block` entries; each block's part of the run is summed from 0 in
+ * order, and the parts are added left to right.  Ids outside [0, vocab)
+ * contribute nothing. */
+void oracle_embed_bwd_tok(const int64_t* ids, int64_t n, const float* dout, int64_t vocab,
+                          int64_t d, int64_t block, float* dtok, int accumulate) {
+  if (!accumulate)
+    for (int64_t i = 0; i < vocab * d; ++i) dtok[i] = 0.0f;
+  /* stable counting sort by id; invalid ids get key vocab (sorted last) */
+  int64_t* start = (int64_t*)calloc((size_t)vocab + 2, sizeof(int64_t));
+  int64_t* order = (int64_t*)malloc((size_t)(n > 0 ? n : 1) * sizeof(int64_t));
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t k = (ids[i] >= 0 && ids[i] < vocab) ? ids[i] : vocab;
+    start[k + 1] += 1;
+  }
+  for (int64_t v = 0; v <= vocab; ++v) start[v + 1] += start[v];
+  {
+    int64_t* fill = (int64_t*)malloc(((size_t)vocab + 1) * sizeof(int64_t));
+    memcpy(fill, start, ((size_t)vocab + 1) * sizeof(int64_t));
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t k = (ids[i] >= 0 && ids[i] < vocab) ? ids[i] : vocab;
+      order[fill[k]++] = i;
+    }
+    free(fill);
+  }
+#pragma omp parallel for schedule(dynamic, 64)
+  for (int64_t v = 0; v < vocab; ++v) {
+    const int64_t a = start[v], b = start[v + 1];
+    if (a == b) continue;
+    for (int64_t c = 0; c < d; ++c) {
+      float total = 0.0f;
+      int first = 1;
+      for (int64_t p0 = a; p0 < b;) {
+        const int64_t p1 = ((p0 / block) + 1) * block < b ? ((p0 / block) + 1) * block : b;
+        float part = 0.0f;
+        for (int64_t p = p0; p < p1; ++p) part = part + dout[order[p] * d + c];
+        total = first ? part : total + part;
+        first = 0;
+        p0 = p1;
+      }
+      dtok[v * d + c] = dtok[v * d + c] + total;
+    }
+  }
+  free(order);
+  free(start);
 }

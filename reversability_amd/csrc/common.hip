@@ -60,6 +60,6 @@ const char* rv_status_string(int status) {
 
 const char* rv_last_error(void) { return g_last_error; }
 
-int rv_abi_version(void) { return 2; }
+int rv_abi_version(void) { return 3; }
 
 }  // extern "C"

@@ -63,8 +63,7 @@ def hidden_states(model, ids, reuse=False):
     """embedding -> core -> final_norm (optimized.py:44-61)."""
     if ids.ndim != 2 or ids.shape[1] > model.config.max_sequence_length:
         raise ValueError("Invalid input shape/context")
-    positions = torch.arange(ids.shape[1], device=ids.device)
-    x = model.token_embedding(ids) + model.position_embedding(positions)
+    x = model.embed(ids)  # token + position embedding (fused once enable_embedding ran)
     if hasattr(model, "core"):
         if reuse:
             if model.method != "midpoint" or model.backward_mode != "reconstruct":

@@ -70,3 +70,21 @@ def test_workspace_size_is_device_independent(rows, width):
     per_block = -(-rows // 256)
     parts = -(-rows // per_block)
     assert n == parts * width * 4
+
+
+def test_embedding_entry_points_validate_without_device():
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4100)  # not 16-byte aligned
+    assert lib.rv_batch_from_tokens(None, 4, 2, fake, fake, None) == 1
+    assert lib.rv_batch_from_tokens(fake, 0, 2, fake, fake, None) == 2
+    assert lib.rv_batch_from_tokens(fake, 4, 0, fake, fake, None) == 2
+    assert lib.rv_embed_fwd(fake, 2, 4, fake, 10, fake, 8, 6, fake, None) == 2   # d % 4
+    assert lib.rv_embed_fwd(fake, 2, 9, fake, 10, fake, 8, 8, fake, None) == 2   # seq > max_seq
+    assert lib.rv_embed_fwd(fake, 2, 4, odd, 10, fake, 8, 8, fake, None) == 3
+    assert lib.rv_embed_fwd(None, 2, 4, fake, 10, fake, 8, 8, fake, None) == 1
+    assert lib.rv_embed_bwd_workspace_bytes(-1, 10, 8) == -2
+    assert lib.rv_embed_bwd_workspace_bytes(16, 10, 6) == -2
+    assert lib.rv_embed_bwd_workspace_bytes(0, 10, 8) == 0
+    assert lib.rv_embed_bwd(fake, 2, 4, odd, 10, 8, 8, fake, 0, fake, 0, fake, 0, None) == 3
+    assert lib.rv_embed_bwd(fake, 2, 4, fake, 0, 8, 8, fake, 0, fake, 0, fake, 0, None) == 2
