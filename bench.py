@@ -245,7 +245,8 @@ def make_train_step(dev, name: str):
     v3 probe path (scripts/benchmark_midpoint_v3.py:78-83 over
     scripts/benchmark_optimized.py:54-82): install_v3 (split core for the
     midpoint config, 8192-token tiled MLP, fused SwiGLU and RMSNorm), the
-    attention projections on the MFMA kernels (enable_linear), the fused token +
+    attention projections and the causal attention itself on the MFMA kernels
+    (enable_linear, enable_attention), the fused token +
     position embedding adding its token gradient into the tied weight's
     gradient (enable_embedding), the batch cut from a uint16 token stream
     resident in HBM (batch_at over DeviceTokens), then
@@ -258,6 +259,7 @@ def make_train_step(dev, name: str):
     import numpy as np
     import torch
     from reversability_amd import build_model
+    from reversability_amd.attention import enable_attention
     from reversability_amd.data import DeviceTokens, batch_at
     from reversability_amd.embedding import enable_embedding
     from reversability_amd.linear import enable_linear
@@ -272,6 +274,7 @@ def make_train_step(dev, name: str):
                          "step_size": cfg["step_size"]}).to(dev)
     install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True)
     enable_linear(model)
+    enable_attention(model)
     enable_embedding(model, into_grad=True)
     opt = FusedAdamW(model.parameters(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
     scaler = torch.amp.GradScaler("cuda")

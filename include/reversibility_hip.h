@@ -283,6 +283,28 @@ int rv_ce_bwd(const void* logits, int dtype, int64_t ld, const int64_t* labels,
               void* stream);
 
 /* ------------------------------------------------------------------------
+ * Causal self-attention (F.scaled_dot_product_attention(q, k, v,
+ * is_causal=True), default scale 1/sqrt(head_dim), src/reversibility/
+ * model.py:40-45) on the packed projection.  qkv fp16 [batch, seq, 3, heads,
+ * head_dim] as the qkv GEMM writes it; out / dout fp16 [batch, seq, heads,
+ * head_dim]; lse fp32 [batch * heads, seq] (base-2 log-sum-exp of the scaled
+ * scores); head_dim 32, 64 or 128; fp16 pointers 16-byte aligned.
+ */
+
+/* out = softmax(q k^T / sqrt(head_dim), causal) v; lse for the backward. */
+int rv_attn_fwd(const void* qkv, int64_t batch, int64_t seq, int64_t heads,
+                int64_t head_dim, void* out, float* lse, void* stream);
+
+/* Workspace bytes of rv_attn_bwd (negative: -error). */
+int64_t rv_attn_bwd_workspace_bytes(int64_t batch, int64_t seq, int64_t heads);
+
+/* dqkv (fp16, qkv's layout) = gradient of out with respect to qkv, given
+ * dout and the forward's out and lse.  Deterministic. */
+int rv_attn_bwd(const void* qkv, const void* out, const void* dout, const float* lse,
+                int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                void* dqkv, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Token pipeline and token + position embedding (the steps in front of the
  * reversible stack).  Tables and activations fp32, d a multiple of 4, fp32
  * pointers 16-byte aligned.

@@ -64,6 +64,9 @@ SIGNATURES = {
     "rv_mlp_dx": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_mlp_wgrad_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "rv_mlp_wgrad": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I, _P, _I64, _P]),
+    "rv_attn_fwd": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "rv_attn_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "rv_attn_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _P]),
     "rv_batch_from_tokens": (_I, [_P, _I64, _I64, _P, _P, _P]),
     "rv_embed_fwd": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _P]),
     "rv_embed_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64]),

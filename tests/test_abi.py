@@ -88,3 +88,17 @@ def test_embedding_entry_points_validate_without_device():
     assert lib.rv_embed_bwd_workspace_bytes(0, 10, 8) == 0
     assert lib.rv_embed_bwd(fake, 2, 4, odd, 10, 8, 8, fake, 0, fake, 0, fake, 0, None) == 3
     assert lib.rv_embed_bwd(fake, 2, 4, fake, 0, 8, 8, fake, 0, fake, 0, fake, 0, None) == 2
+
+
+def test_attention_entry_points_validate_without_device():
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4104)
+    assert lib.rv_attn_fwd(None, 2, 16, 2, 32, fake, fake, None) == 1
+    assert lib.rv_attn_fwd(fake, 0, 16, 2, 32, fake, fake, None) == 2
+    assert lib.rv_attn_fwd(fake, 2, 16, 2, 16, fake, fake, None) == 3   # head_dim 16
+    assert lib.rv_attn_fwd(odd, 2, 16, 2, 64, fake, fake, None) == 3
+    assert lib.rv_attn_bwd_workspace_bytes(2, 16, 3) == 2 * 16 * 3 * 4
+    assert lib.rv_attn_bwd_workspace_bytes(0, 16, 3) == -2
+    assert lib.rv_attn_bwd(fake, fake, fake, fake, 2, 16, 2, 64, fake, fake, 4, None) == 4
+    assert lib.rv_attn_bwd(fake, fake, fake, fake, 2, 16, 2, 48, fake, fake, 1 << 20, None) == 3

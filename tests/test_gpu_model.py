@@ -23,6 +23,7 @@ import torch.nn.functional as F
 
 from reconstruction_gate import TOLERANCES, check_case
 from reversability_amd import build_model
+from reversability_amd.attention import enable_attention
 from reversability_amd.embedding import enable_embedding
 from reversability_amd.kernels_v3 import FusedRMSNorm
 from reversability_amd.linear import enable_linear
@@ -253,7 +254,8 @@ def test_full_midpoint_step_matches_autograd(cuda_device, core):
 
 def test_bench_path_step_matches_autograd(cuda_device):
     """The measured training step's path -- split core, tiled MLP, fused SwiGLU
-    and RMSNorm, MFMA attention projections, fused embedding adding into the
+    and RMSNorm, MFMA attention projections and causal attention, fused
+    embedding adding into the
     tied gradient, cached head with the fused
     cross-entropy over the whole batch -- against eager autograd of the same
     model with F.cross_entropy (loss within 2e-3, every parameter gradient
@@ -264,6 +266,7 @@ def test_bench_path_step_matches_autograd(cuda_device):
     reference.backward_mode = "autograd"
     install_v3(candidate, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
     enable_linear(candidate)
+    enable_attention(candidate)
     enable_embedding(candidate, into_grad=True)
     x, y = _c4_batch(cuda_device)
     loss_r, grads_r = _step_grads(reference, x, y)
