@@ -85,6 +85,8 @@ def parse_args():
                    help="only the kernel loop (used under rocprofv3)")
     p.add_argument("--mlp-only", action="store_true",
                    help="only the MLP block and MLP GEMM measurements (used under rocprofv3)")
+    p.add_argument("--attn-only", action="store_true",
+                   help="only the attention and embedding measurements (used under rocprofv3)")
     return p.parse_args()
 
 
@@ -405,6 +407,99 @@ def mlp_block_bench(dev, steps: int = 20):
             "algorithmic_flop": flops}
 
 
+ATTN_SHAPES = {  # (batch, seq, heads, head_dim) of the attention inside configs[3] / [4]
+    "c4_b33_t512_h8_d32": (33, 512, 8, 32),
+    "c5_b16_t2048_h16_d64": (16, 2048, 16, 64),
+}
+
+
+def attention_bench(dev, reps: int = 20):
+    """Causal attention kernels alone (rv_attn_fwd, rv_attn_bwd on the packed
+    qkv) at the configs' shapes, with torch's scaled_dot_product_attention on
+    the same inputs beside them.  Algorithmic flop, causal: forward
+    4 B H hd T (T + 1) / 2 (the two products over the lower triangle),
+    backward 2.5x that (dV, dP, dQ, dK and one recomputation of S)."""
+    import torch
+    from reversability_amd import attention
+    from reversability_amd._hip import _stream, library
+    lib = library()
+    out = {}
+    for name, (b, t, h, hd) in ATTN_SHAPES.items():
+        g = torch.Generator(device=dev).manual_seed(1337)
+        qkv = (0.5 * torch.randn(b, t, 3 * h * hd, device=dev, generator=g)).half()
+        dout = torch.randn(b, t, h * hd, device=dev, generator=g).half()
+        o = torch.empty(b, t, h * hd, device=dev, dtype=torch.float16)
+        lse = torch.empty(b * h, t, device=dev)
+        dqkv = torch.empty_like(qkv)
+        ws = torch.empty(lib.rv_attn_bwd_workspace_bytes(b, t, h) // 4, device=dev)
+        st = _stream(qkv)
+
+        def fwd():
+            lib.rv_attn_fwd(qkv.data_ptr(), b, t, h, hd, o.data_ptr(), lse.data_ptr(), st)
+
+        def bwd():
+            lib.rv_attn_bwd(qkv.data_ptr(), o.data_ptr(), dout.data_ptr(), lse.data_ptr(), b, t,
+                            h, hd, dqkv.data_ptr(), ws.data_ptr(), ws.numel() * 4, st)
+
+        fwd()
+        f_us, b_us = _event_time_us(fwd, reps), _event_time_us(bwd, reps)
+        x = qkv.clone().requires_grad_(True)
+
+        def torch_fb():
+            x.grad = None
+            attention.reference_attention(x, h).backward(dout)
+
+        def torch_f():
+            attention.reference_attention(qkv, h)
+
+        tf_us, tfb_us = _event_time_us(torch_f, reps), _event_time_us(torch_fb, reps)
+        flop = 4 * b * h * hd * t * (t + 1) // 2
+        out[name] = {
+            "fwd_us": round(f_us, 1), "bwd_us": round(b_us, 1),
+            "fwd_TFLOPs": round(flop / f_us / 1e6, 1),
+            "bwd_TFLOPs": round(2.5 * flop / b_us / 1e6, 1),
+            "fwd_frac": round(flop / f_us / 1e6 / MFMA_PEAK_TFLOPS, 4),
+            "bwd_frac": round(2.5 * flop / b_us / 1e6 / MFMA_PEAK_TFLOPS, 4),
+            "torch_sdpa_fwd_us": round(tf_us, 1), "torch_sdpa_fwd_bwd_us": round(tfb_us, 1),
+            "algorithmic_fwd_flop": flop}
+    return out
+
+
+def embedding_bench(dev, reps: int = 20):
+    """Token pipeline and embedding kernels alone at configs[4]'s shape
+    (16 x 2048 tokens, d 1024, vocab 50257, uniform ids): batch_at from an
+    HBM-resident uint16 stream, forward (token rows read, output written:
+    8 d bytes per token) and backward adding into an existing token-table
+    gradient (dout read twice -- token and position sums -- and each touched
+    token row read and written: at most 16 d bytes per token)."""
+    import numpy as np
+    import torch
+    from reversability_amd import data, embedding
+    b, t, d, vocab = 16, 2048, 1024, 50257
+    stream = np.random.default_rng(1337).integers(0, vocab, b * t + 1).astype(np.uint16)
+    tokens = data.DeviceTokens(stream, dev)
+    x, _, _ = data.batch_at(tokens, 0, b, t, b * t)
+    g = torch.Generator(device=dev).manual_seed(1337)
+    tok = (0.02 * torch.randn(vocab, d, device=dev, generator=g)).requires_grad_(True)
+    pos = (0.02 * torch.randn(t, d, device=dev, generator=g)).requires_grad_(True)
+    dout = torch.randn(b, t, d, device=dev, generator=g)
+    tok.grad = torch.zeros_like(tok)
+    n = b * t
+    fwd_us = _event_time_us(lambda: embedding.embed(x, tok.detach(), pos.detach()), reps)
+    y = embedding.embed(x, tok, pos, into_grad=True)
+
+    def bwd():
+        pos.grad = None
+        torch.autograd.backward(y, dout, retain_graph=True)
+
+    bwd_us = _event_time_us(bwd, reps)
+    batch_us = _event_time_us(lambda: data.batch_at(tokens, 0, b, t, b * t), reps)
+    return {"workload": "configs[4] embedding 16x2048 d1024 vocab 50257",
+            "batch_at_us": round(batch_us, 1),
+            "fwd_us": round(fwd_us, 1), "fwd_GBps": round(8 * d * n / fwd_us / 1e3, 1),
+            "bwd_us": round(bwd_us, 1), "bwd_GBps_upper": round(16 * d * n / bwd_us / 1e3, 1)}
+
+
 def cpu_baseline(seconds: float):
     """Oracle (C, OpenMP) on this host's cores: the same RMSNorm+SwiGLU step."""
     import numpy as np
@@ -469,6 +564,10 @@ def main() -> int:
         print(json.dumps({"mlp_block": mlp_block_bench(dev), "mlp_gemms": mlp_gemm_bench(dev)}),
               flush=True)
         return 0
+    if args.attn_only:
+        print(json.dumps({"attention": attention_bench(dev), "embedding": embedding_bench(dev)}),
+              flush=True)
+        return 0
     ms_step_s, per_kernel = time_kernels(dev, args.steps, args.warmup)
     value = STEP_BYTES / ms_step_s / 1e9
     bytes_by = {"rms_fwd": RMS_FWD_BYTES, "rms_bwd": RMS_BWD_BYTES,
@@ -505,8 +604,10 @@ def main() -> int:
     if not args.no_train_step:
         line["mlp_block"] = mlp_block_bench(dev)
         line["mlp_gemms"] = mlp_gemm_bench(dev)
+        line["attention"] = attention_bench(dev)
+        line["embedding"] = embedding_bench(dev)
         line["train_step"] = train_step_bench(dev, args.train_steps, args.train_warmup)
-        line["train_step_c5"] = train_step_bench(dev, 3, 2, "c5")
+        line["train_step_c5"] = train_step_bench(dev, 5, 2, "c5")
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
