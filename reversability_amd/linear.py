@@ -25,7 +25,7 @@ import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
 from ._hip import RV_F16, RV_F32, _check, _stream, library
-from .mlp import cast_f16
+from .mlp import cast_f16, cast_weight
 
 
 def supported(x: torch.Tensor, weight: torch.Tensor, bias) -> bool:
@@ -48,7 +48,7 @@ class FusedLinear(torch.autograd.Function):
         x16 = cast_f16(flat.contiguous())
         y = torch.empty(rows, out_f, device=x.device, dtype=torch.float16)
         if rows:
-            w16 = cast_f16(weight)
+            w16 = cast_weight(weight)
             _check(library().rv_linear_fwd(x16.data_ptr(), in_f, w16.data_ptr(), rows, in_f,
                                            out_f, y.data_ptr(), _stream(x)), "rv_linear_fwd")
         ctx.save_for_backward(x16, weight)
@@ -68,7 +68,7 @@ class FusedLinear(torch.autograd.Function):
             return (torch.zeros(ctx.x_shape, device=dy.device, dtype=ctx.x_dtype),
                     torch.zeros_like(weight))
         if ctx.needs_input_grad[0]:
-            w16 = cast_f16(weight)
+            w16 = cast_weight(weight)
             dx = torch.empty(rows, in_f, device=dy.device, dtype=ctx.x_dtype)
             code = RV_F32 if ctx.x_dtype == torch.float32 else RV_F16
             _check(lib.rv_linear_dx(dy.data_ptr(), w16.data_ptr(), rows, in_f, out_f,

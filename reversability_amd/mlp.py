@@ -19,6 +19,8 @@ torch's GEMMs otherwise.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 from ._hip import _check, _stream, library
@@ -43,6 +45,47 @@ def cast_f16(t: torch.Tensor) -> torch.Tensor:
     _check(library().rv_cast_f32_f16(t.data_ptr(), out.data_ptr(), t.numel(), _stream(t)),
            "rv_cast_f32_f16")
     return out
+
+
+# Call-scoped cache of fp16 weight casts (see weight_cast_cache).
+_weight_cache: dict | None = None
+
+
+@contextlib.contextmanager
+def weight_cast_cache():
+    """Reuse fp16 casts of the same fp32 weight inside this block.
+
+    A training step evaluates each layer's force several times -- forward,
+    the reconstruction's inverse, the recompute for the VJP -- and each
+    evaluation cast every weight again.  Inside the block, ``cast_weight``
+    casts a given weight tensor once and hands out that copy afterwards
+    (what autocast's own cast cache does within one autocast region).  The
+    weights must not be modified inside the block; the trainers open it
+    around one forward + backward, before the optimizer step.  Nested blocks
+    share the outer cache.
+    """
+    global _weight_cache
+    if _weight_cache is not None:
+        yield
+        return
+    _weight_cache = {}
+    try:
+        yield
+    finally:
+        _weight_cache = None
+
+
+def cast_weight(w: torch.Tensor) -> torch.Tensor:
+    """``cast_f16(w)``, reused inside a ``weight_cast_cache`` block."""
+    cache = _weight_cache
+    if cache is None:
+        return cast_f16(w)
+    hit = cache.get(id(w))
+    if hit is not None and hit[0] is w:
+        return hit[1]
+    w16 = cast_f16(w)
+    cache[id(w)] = (w, w16)  # the strong reference keeps id(w) unique in the block
+    return w16
 
 
 def _f16(t: torch.Tensor, what: str) -> None:

@@ -100,6 +100,14 @@ def chunked_backward(model, ids, labels, denominator, chunk_tokens, scaler=None,
     """
     if chunk_tokens <= 0 or denominator <= 0:
         raise ValueError("Chunk size and normalization denominator must be positive")
+    from .mlp import weight_cast_cache
+    with weight_cast_cache():  # weights are constant until the optimizer step
+        return _chunked_backward(model, ids, labels, denominator, chunk_tokens, scaler,
+                                 precision, reuse, loss_backend)
+
+
+def _chunked_backward(model, ids, labels, denominator, chunk_tokens, scaler, precision, reuse,
+                      loss_backend):
     with amp_context(ids.device, precision):
         hidden = hidden_states(model, ids, reuse)
     leaf = hidden.detach().reshape(-1, hidden.shape[-1]).requires_grad_(True)

@@ -114,7 +114,7 @@ class TiledMLP(torch.autograd.Function):
             # autocast's casts, once per call: the same fp16 values F.linear
             # would produce on every tile
             x16 = mlp.cast_f16(flat.contiguous())
-            up16, down16 = mlp.cast_f16(up), mlp.cast_f16(down)
+            up16, down16 = mlp.cast_weight(up), mlp.cast_weight(down)
             for start in range(0, flat.shape[0], tokens):
                 o, _ = mlp.up_swiglu(x16[start:start + tokens], up16)
                 mlp.down(o, down16, output[start:start + tokens])
@@ -142,7 +142,7 @@ class TiledMLP(torch.autograd.Function):
         if _use_mfma(flat, up, down, ctx.fused, cdt):
             from . import mlp
             x16, dy = mlp.cast_f16(flat.contiguous()), dy.contiguous()
-            up16, down16 = mlp.cast_f16(up), mlp.cast_f16(down)
+            up16, down16 = mlp.cast_weight(up), mlp.cast_weight(down)
             dup, ddown = torch.empty_like(up), torch.empty_like(down)
             for i, start in enumerate(range(0, flat.shape[0], ctx.tokens)):
                 stop = start + ctx.tokens
@@ -281,6 +281,14 @@ def cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler=N
     weight dtype before it is added to the tied ``.grad``."""
     if reuse or chunk_tokens < 1 or denominator < 1:
         raise ValueError("Use installed core mode and positive normalization/chunk")
+    from . import mlp
+    with mlp.weight_cast_cache():  # weights are constant until the optimizer step
+        return _cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler,
+                                     precision, loss_backend)
+
+
+def _cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler, precision,
+                          loss_backend):
     with amp_context(ids.device, precision):
         hidden = hidden_states(model, ids)
     leaf = hidden.detach().reshape(-1, hidden.shape[-1]).requires_grad_(True)

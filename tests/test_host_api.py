@@ -355,3 +355,28 @@ def test_reconstruction_under_autocast_backward_outside_context(core):
         assert b.grad is not None, name
         rel = float((a.grad - b.grad).norm() / a.grad.norm().clamp_min(1e-12))
         assert rel < 2e-2, (name, rel)
+
+
+def test_weight_cast_cache_scope():
+    """cast_weight reuses a cast only inside weight_cast_cache, keyed on the
+    tensor object itself (CPU: the cast's launcher is replaced by a stub)."""
+    import torch
+    from reversability_amd import mlp
+    calls = []
+    original = mlp.cast_f16
+    mlp.cast_f16 = lambda t: calls.append(t) or t.half()
+    try:
+        w, v = torch.ones(4, 4), torch.ones(4, 4)
+        mlp.cast_weight(w), mlp.cast_weight(w)
+        assert len(calls) == 2          # no cache outside the block
+        with mlp.weight_cast_cache():
+            a = mlp.cast_weight(w)
+            with mlp.weight_cast_cache():   # nested blocks share the cache
+                assert mlp.cast_weight(w) is a
+            assert mlp.cast_weight(v) is not a
+            assert mlp.cast_weight(w) is a
+        assert len(calls) == 4
+        mlp.cast_weight(w)
+        assert len(calls) == 5          # the cache ends with the outer block
+    finally:
+        mlp.cast_f16 = original
