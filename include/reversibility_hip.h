@@ -144,6 +144,21 @@ int rv_residual_axpy(const void* x, const void* f, void* out, int sign,
                      int64_t n, int state_dtype, int force_dtype,
                      void* stream);
 
+/* rv_rmsnorm_fwd with y written as fp16 (rounded to nearest even): the
+ * value fp16 autocast feeds the GEMM that consumes y (FusedRMSNorm's output
+ * under torch.autocast(float16), src/reversibility/kernels_v3.py:51-83).
+ * width % 4 == 0; x, w 16-byte aligned, y 8-byte aligned. */
+int rv_rmsnorm_fwd_f16(const float* x, const float* w, void* y, float* rstd,
+                       int64_t rows, int64_t width, float eps, void* stream);
+
+/* rv_rmsnorm_bwd with dy given as fp16 (the consuming GEMM's input gradient,
+ * which autocast widens to fp32 without change); same results bit for bit.
+ * width % 4 == 0; x, w, dx 16-byte aligned, dy 8-byte aligned. */
+int rv_rmsnorm_bwd_f16(const float* x, const float* w, const void* dy,
+                       const float* rstd, float* dx, float* dw, void* workspace,
+                       int64_t workspace_bytes, int64_t rows, int64_t width,
+                       void* stream);
+
 /* Fused residual add + RMSNorm (the x + A(x) -> mlp_norm step of
  * midpoint_force and the q' = q + A(p) -> mlp_norm step of Euler):
  *   h[r, :] = x[r, :] + S(f[r, :])             (written to h)

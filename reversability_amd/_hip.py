@@ -42,6 +42,8 @@ SIGNATURES = {
     "rv_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_rmsnorm_bwd_workspace_bytes": (_I64, [_I64, _I64]),
     "rv_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rv_rmsnorm_fwd_f16": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _P]),
+    "rv_rmsnorm_bwd_f16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rv_swiglu_fwd": (_I, [_P, _I64, _P, _I64, _I64, _I, _P]),
     "rv_swiglu_bwd": (_I, [_P, _I64, _P, _P, _I64, _I64, _I, _P]),
     "rv_midpoint_update": (_I, [_P, _P, _P, _P, _D, _I, _I64, _I, _I, _P]),
@@ -167,16 +169,16 @@ class _DeviceGuard:
 # Kernel launchers (CUDA tensors, validated by the callers' autograd Functions)
 # ---------------------------------------------------------------------------
 
-def _rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float):
+def _rmsnorm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float, fp16_out: bool = False):
     width = x.shape[-1]
     rows = x.numel() // width if width else 0
-    y = torch.empty_like(x)
+    y = torch.empty_like(x, dtype=torch.float16 if fp16_out else x.dtype)
     rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
     if rows:
+        fn = library().rv_rmsnorm_fwd_f16 if fp16_out else library().rv_rmsnorm_fwd
         with _DeviceGuard(x):
-            _check(library().rv_rmsnorm_fwd(x.data_ptr(), w.data_ptr(), y.data_ptr(),
-                                            rstd.data_ptr(), rows, width, eps, _stream(x)),
-                   "rv_rmsnorm_fwd")
+            _check(fn(x.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, width,
+                      eps, _stream(x)), "rv_rmsnorm_fwd")
     return y, rstd
 
 
@@ -196,8 +198,9 @@ def _rmsnorm_bwd(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch
     dw = torch.empty_like(w)
     nbytes = rmsnorm_workspace_bytes(rows, width)
     ws = torch.empty(nbytes // 4, device=x.device, dtype=torch.float32)
+    fn = library().rv_rmsnorm_bwd_f16 if dy.dtype == torch.float16 else library().rv_rmsnorm_bwd
     with _DeviceGuard(x):
-        _check(library().rv_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
+        _check(fn(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
                                         rstd.data_ptr(), dx.data_ptr(), dw.data_ptr(),
                                         ws.data_ptr(), nbytes, rows, width, _stream(x)),
                "rv_rmsnorm_bwd")
@@ -314,7 +317,8 @@ def _ce_bwd(logits: torch.Tensor, labels: torch.Tensor, rmax: torch.Tensor, rlse
 NAMESPACE = "reversability_amd"
 _library = torch.library.Library(NAMESPACE, "DEF")
 _SCHEMAS = {
-    "rmsnorm_fwd": ("rmsnorm_fwd(Tensor x, Tensor weight, float eps) -> (Tensor, Tensor)", _rmsnorm_fwd),
+    "rmsnorm_fwd": ("rmsnorm_fwd(Tensor x, Tensor weight, float eps, bool fp16_out=False) "
+                    "-> (Tensor, Tensor)", _rmsnorm_fwd),
     "rmsnorm_bwd": ("rmsnorm_bwd(Tensor x, Tensor weight, Tensor dy, Tensor rstd) -> (Tensor, Tensor)",
                     _rmsnorm_bwd),
     "add_rmsnorm_fwd": ("add_rmsnorm_fwd(Tensor x, Tensor f, Tensor weight, float eps) -> (Tensor, Tensor, Tensor)",
@@ -342,8 +346,9 @@ def _fake_rows(x):
 
 
 @torch.library.register_fake(f"{NAMESPACE}::rmsnorm_fwd")
-def _(x, weight, eps):
-    return torch.empty_like(x), x.new_empty(_fake_rows(x), dtype=torch.float32)
+def _(x, weight, eps, fp16_out=False):
+    return (torch.empty_like(x, dtype=torch.float16 if fp16_out else x.dtype),
+            x.new_empty(_fake_rows(x), dtype=torch.float32))
 
 
 @torch.library.register_fake(f"{NAMESPACE}::rmsnorm_bwd")

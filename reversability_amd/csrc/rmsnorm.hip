@@ -12,10 +12,19 @@
 // of dw ([nparts][width]).  A second small kernel sums each column's partials
 // in a fixed order.
 //
+// Under fp16 autocast the normalized output's only consumers are fp16 GEMMs,
+// which read it through autocast's fp16 cast; the _f16 entry points write that
+// fp16 value directly (y rounded to nearest even, the cast's rounding) and take
+// the incoming gradient as fp16 (the GEMM's fp16 product, which autocast widens
+// to fp32 unchanged), so the results are bit-identical to the fp32 y / dy path
+// followed by the cast, with half of y's and dy's bytes and no cast launch.
+//
 // Arithmetic follows src/reversibility/kernels_v3.py:9-48 operation by
 // operation (sum/width + eps, x*r*w, g*x reduction, (g - x*c)*r, and the
 // forward multiply order x*r inside the dweight sum); the build disables FMA
 // contraction to match the reference's enable_fp_fusion=False.
+
+#include <type_traits>
 
 #include "rv_device.h"
 
@@ -60,6 +69,22 @@ constexpr int kMaxEpl = 64;      // scalar path: elements per lane <= 64
 // branch) and never stored.  With ADD the row input is x + float(f) (fused
 // residual add) and that sum is also written to h.
 // ---------------------------------------------------------------------------
+// Four normalized values to y (fp32: one streaming 16-byte store; fp16:
+// rounded to nearest even, one streaming 8-byte store).  The fp16 values are
+// the fp32 products rounded once more: without the empty asm the compiler
+// folds "fp16(a * b)" into v_fma_mixlo_f16, a single rounding of the exact
+// product, which differs from autocast's cast of the fp32 y.
+__device__ __forceinline__ void store_y(float* p, float4 v) { rv::st_f4s(p, v); }
+__device__ __forceinline__ void store_y(__half* p, float4 v) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+  const uint32_t lo = (uint32_t)__half_as_ushort(__float2half_rn(v.x)) |
+                      ((uint32_t)__half_as_ushort(__float2half_rn(v.y)) << 16);
+  const uint32_t hi = (uint32_t)__half_as_ushort(__float2half_rn(v.z)) |
+                      ((uint32_t)__half_as_ushort(__float2half_rn(v.w)) << 16);
+  __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(p));
+}
+
 template <int VEC, int RPW, typename F, bool ADD>
 struct RowTile {
   float4 x[RPW][VEC];
@@ -83,9 +108,9 @@ __device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD>& t, const flo
   }
 }
 
-template <int VEC, int RPW, typename F, bool ADD>
+template <int VEC, int RPW, typename F, bool ADD, typename Y>
 __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const float4 (&wv)[VEC],
-                                           float* __restrict__ h, float* __restrict__ y,
+                                           float* __restrict__ h, Y* __restrict__ y,
                                            float* __restrict__ rstd, int64_t row0, int64_t rows,
                                            int width, float eps, int lane) {
 #pragma unroll
@@ -120,7 +145,7 @@ __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const f
           o.y = (q.y * rs) * wv[v].y;
           o.z = (q.z * rs) * wv[v].z;
           o.w = (q.w * rs) * wv[v].w;
-          rv::st_f4s(y + row * width + col, o);
+          store_y(y + row * width + col, o);
           if constexpr (ADD) rv::st_f4s(h + row * width + col, q);
         }
       }
@@ -129,11 +154,11 @@ __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const f
   }
 }
 
-template <int VEC, int RPW, typename F, bool ADD>
+template <int VEC, int RPW, typename F, bool ADD, typename Y>
 __global__ __launch_bounds__(kFwdWaves * 64)
 void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
                  const float* __restrict__ w, float* __restrict__ h,
-                 float* __restrict__ y, float* __restrict__ rstd,
+                 Y* __restrict__ y, float* __restrict__ rstd,
                  int64_t rows, int width, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * kFwdWaves;
@@ -216,9 +241,9 @@ struct BwdTile {
   float rs[2];
 };
 
-template <int VEC>
+template <int VEC, typename G>
 __device__ __forceinline__ void bwd_load(BwdTile<VEC>& t, const float* __restrict__ x,
-                                         const float* __restrict__ dy,
+                                         const G* __restrict__ dy,
                                          const float* __restrict__ rstd, int64_t row0,
                                          int64_t end, int width, int lane) {
 #pragma unroll
@@ -230,7 +255,7 @@ __device__ __forceinline__ void bwd_load(BwdTile<VEC>& t, const float* __restric
       const int col = (v * 64 + lane) * 4;
       const int col_c = col < width ? col : width - 4;
       t.x[r][v] = rv::ld_f4(x + row * width + col_c);
-      t.g[r][v] = rv::ld_f4(dy + row * width + col_c);
+      t.g[r][v] = rv::load4f(dy + row * width + col_c);
     }
   }
 }
@@ -286,10 +311,10 @@ __device__ __forceinline__ void bwd_finish(BwdTile<VEC>& t, const float4 (&wv)[V
 
 // WAVES per block: wide rows keep fewer waves so that their two-row
 // ping-pong tiles stay in registers (no scratch).
-template <int VEC, int WAVES>
+template <int VEC, int WAVES, typename G>
 __global__ __launch_bounds__(WAVES * 64)
 void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
-                 const float* __restrict__ dy, const float* __restrict__ rstd,
+                 const G* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
                  int64_t rows, int width, int64_t rows_per_block) {
   const int lane = threadIdx.x & 63;
@@ -464,12 +489,13 @@ BwdPlan plan_bwd(int64_t rows) {
   return p;
 }
 
-template <typename F, bool ADD>
-int launch_fwd(const float* x, const F* f, const float* w, float* h, float* y,
+template <typename F, bool ADD, typename Y = float>
+int launch_fwd(const float* x, const F* f, const float* w, float* h, Y* y,
                float* rstd, int64_t rows, int width, float eps,
                hipStream_t stream) {
   const bool vec = (width % 4 == 0) && rv_host::aligned16(x) &&
-                   rv_host::aligned16(w) && rv_host::aligned16(y) &&
+                   rv_host::aligned16(w) &&
+                   (reinterpret_cast<uintptr_t>(y) % (4 * sizeof(Y))) == 0 &&
                    (h == nullptr || rv_host::aligned16(h)) &&
                    (f == nullptr ||
                     (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0);
@@ -483,7 +509,7 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, float* y,
     const dim3 block(kFwdWaves * 64);
     const int vecs = (width + 255) / 256;
 #define RV_FWD_VEC(V)                                                          \
-  hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, ADD>), grid, block, 0, stream, x, f, \
+  hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, ADD, Y>), grid, block, 0, stream, x, f, \
                      w, h, y, rstd, rows, width, eps)
     if (vecs <= 1) RV_FWD_VEC(1);
     else if (vecs <= 2) RV_FWD_VEC(2);
@@ -493,6 +519,9 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, float* y,
 #undef RV_FWD_VEC
     return rv_host::check_launch();
   }
+  if constexpr (!std::is_same<Y, float>::value) {
+    return RV_ERR_UNSUPPORTED;  // fp16 output: vector path only
+  } else {
   if (width > 64 * kMaxEpl) return RV_ERR_UNSUPPORTED;
   const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
   const dim3 block(kFwdWaves * 64);
@@ -508,6 +537,60 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, float* y,
   else if (epl <= 32) RV_FWD_SC(32);
   else RV_FWD_SC(64);
 #undef RV_FWD_SC
+  return rv_host::check_launch();
+  }
+}
+
+template <typename G>
+int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, float* dx,
+               float* dw, void* workspace, int64_t workspace_bytes, int64_t rows,
+               int64_t width, hipStream_t s) {
+  if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096) return RV_ERR_UNSUPPORTED;
+  const BwdPlan p = plan_bwd(rows);
+  const int64_t need = (int64_t)p.nparts * width * (int64_t)sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
+  if (!rv_host::aligned16(workspace)) return RV_ERR_WORKSPACE;
+  float* partial = (float*)workspace;
+  const dim3 grid((unsigned)p.nparts);
+  const dim3 block(kBwdWaves * 64);
+  const int iw = (int)width;
+  const bool vec = (width % 4 == 0) && rv_host::aligned16(x) &&
+                   rv_host::aligned16(w) &&
+                   (reinterpret_cast<uintptr_t>(dy) % (4 * sizeof(G))) == 0 &&
+                   rv_host::aligned16(dx);
+  if (vec) {
+    const int vecs = (iw + 255) / 256;
+#define RV_BWD_VEC(V)                                                             \
+  hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V), G>), grid, dim3(bwd_waves(V) * 64), 0, s, x, \
+                     w, dy, rstd, dx, partial, rows, iw, p.rows_per_block)
+    if (vecs <= 1) RV_BWD_VEC(1);
+    else if (vecs <= 2) RV_BWD_VEC(2);
+    else if (vecs <= 4) RV_BWD_VEC(4);
+    else if (vecs <= 8) RV_BWD_VEC(8);
+    else RV_BWD_VEC(16);
+#undef RV_BWD_VEC
+  } else if constexpr (!std::is_same<G, float>::value) {
+    return RV_ERR_UNSUPPORTED;  // fp16 gradient: vector path only
+  } else {
+    const int epl = (iw + 63) / 64;
+#define RV_BWD_SC(E)                                                          \
+  hipLaunchKernelGGL((rms_bwd_scalar<E>), grid, block, 0, s, x, w, dy, rstd, dx, \
+                     partial, rows, iw, p.rows_per_block)
+    if (epl <= 1) RV_BWD_SC(1);
+    else if (epl <= 2) RV_BWD_SC(2);
+    else if (epl <= 4) RV_BWD_SC(4);
+    else if (epl <= 8) RV_BWD_SC(8);
+    else if (epl <= 16) RV_BWD_SC(16);
+    else if (epl <= 32) RV_BWD_SC(32);
+    else RV_BWD_SC(64);
+#undef RV_BWD_SC
+  }
+  int st = rv_host::check_launch();
+  if (st != RV_OK) return st;
+  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 63) / 64)),
+                     dim3(kRedWaves * 64), 0, s, partial, dw, iw, p.nparts);
   return rv_host::check_launch();
 }
 
@@ -557,51 +640,24 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
                    const float* rstd, float* dx, float* dw, void* workspace,
                    int64_t workspace_bytes, int64_t rows, int64_t width,
                    void* stream) {
-  if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
+  return launch_bwd<float>(x, w, dy, rstd, dx, dw, workspace, workspace_bytes, rows, width,
+                           (hipStream_t)stream);
+}
+
+int rv_rmsnorm_fwd_f16(const float* x, const float* w, void* y, float* rstd, int64_t rows,
+                       int64_t width, float eps, void* stream) {
+  if (!x || !w || !y || !rstd) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > 4096) return RV_ERR_UNSUPPORTED;
-  const BwdPlan p = plan_bwd(rows);
-  const int64_t need = (int64_t)p.nparts * width * (int64_t)sizeof(float);
-  if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
-  if (!rv_host::aligned16(workspace)) return RV_ERR_WORKSPACE;
-  float* partial = (float*)workspace;
-  const hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)p.nparts);
-  const dim3 block(kBwdWaves * 64);
-  const int iw = (int)width;
-  const bool vec = (width % 4 == 0) && rv_host::aligned16(x) &&
-                   rv_host::aligned16(w) && rv_host::aligned16(dy) &&
-                   rv_host::aligned16(dx);
-  if (vec) {
-    const int vecs = (iw + 255) / 256;
-#define RV_BWD_VEC(V)                                                             \
-  hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V)>), grid, dim3(bwd_waves(V) * 64), 0, s, x, \
-                     w, dy, rstd, dx, partial, rows, iw, p.rows_per_block)
-    if (vecs <= 1) RV_BWD_VEC(1);
-    else if (vecs <= 2) RV_BWD_VEC(2);
-    else if (vecs <= 4) RV_BWD_VEC(4);
-    else if (vecs <= 8) RV_BWD_VEC(8);
-    else RV_BWD_VEC(16);
-#undef RV_BWD_VEC
-  } else {
-    const int epl = (iw + 63) / 64;
-#define RV_BWD_SC(E)                                                          \
-  hipLaunchKernelGGL((rms_bwd_scalar<E>), grid, block, 0, s, x, w, dy, rstd, dx, \
-                     partial, rows, iw, p.rows_per_block)
-    if (epl <= 1) RV_BWD_SC(1);
-    else if (epl <= 2) RV_BWD_SC(2);
-    else if (epl <= 4) RV_BWD_SC(4);
-    else if (epl <= 8) RV_BWD_SC(8);
-    else if (epl <= 16) RV_BWD_SC(16);
-    else if (epl <= 32) RV_BWD_SC(32);
-    else RV_BWD_SC(64);
-#undef RV_BWD_SC
-  }
-  int st = rv_host::check_launch();
-  if (st != RV_OK) return st;
-  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 63) / 64)),
-                     dim3(kRedWaves * 64), 0, s, partial, dw, iw, p.nparts);
-  return rv_host::check_launch();
+  return launch_fwd<float, false, __half>(x, nullptr, w, nullptr, static_cast<__half*>(y), rstd,
+                                          rows, (int)width, eps, (hipStream_t)stream);
+}
+
+int rv_rmsnorm_bwd_f16(const float* x, const float* w, const void* dy, const float* rstd,
+                       float* dx, float* dw, void* workspace, int64_t workspace_bytes,
+                       int64_t rows, int64_t width, void* stream) {
+  return launch_bwd<__half>(x, w, static_cast<const __half*>(dy), rstd, dx, dw, workspace,
+                            workspace_bytes, rows, width, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -29,13 +29,26 @@ def _validate(x: torch.Tensor, weight: torch.Tensor) -> None:
         raise ValueError("Contiguous input and one-dimensional matching norm weight required")
 
 
+def _fp16_out(x: torch.Tensor) -> bool:
+    """fp16 output applies under fp16 autocast on rows the vector kernels cover."""
+    return (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.float16
+            and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0)
+
+
 class FusedRMSNorm(torch.autograd.Function):
-    """``y = x * rsqrt(mean(x^2) + eps) * weight`` over the last dimension."""
+    """``y = x * rsqrt(mean(x^2) + eps) * weight`` over the last dimension.
+
+    ``fp16_out=True`` (a fourth, optional argument; the reference's three-argument
+    call is unchanged) is for norms whose only consumers are fp16-autocast GEMMs:
+    under fp16 autocast y is returned as the fp16 value autocast would feed
+    those GEMMs, and the incoming fp16 gradient is taken as is -- bit-identical
+    results without the fp32 y, its cast, or the fp32 gradient."""
 
     @staticmethod
-    def forward(ctx, x, weight, eps):
+    def forward(ctx, x, weight, eps, fp16_out=False):
         _validate(x, weight)
-        output, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps))
+        half = bool(fp16_out) and _fp16_out(x)
+        output, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps), half)
         ctx.save_for_backward(x, weight, rstd)
         return output
 
@@ -43,8 +56,10 @@ class FusedRMSNorm(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, gradient):
         x, weight, rstd = ctx.saved_tensors
+        if gradient.dtype not in (torch.float32, torch.float16):
+            gradient = gradient.float()
         dx, dweight = ops.rmsnorm_bwd(x, weight.contiguous(), gradient.contiguous(), rstd)
-        return dx, dweight, None
+        return dx, dweight, None, None
 
 
 def rms_norm_eps(module: torch.nn.RMSNorm, x: torch.Tensor) -> float:
@@ -52,10 +67,12 @@ def rms_norm_eps(module: torch.nn.RMSNorm, x: torch.Tensor) -> float:
     return module.eps if module.eps is not None else torch.finfo(x.dtype).eps
 
 
-def enable_rmsnorm(model: torch.nn.Module) -> None:
-    """Route every nn.RMSNorm of ``model`` through FusedRMSNorm (kernels_v3.py:77-83)."""
+def enable_rmsnorm(model: torch.nn.Module, fp16_out: bool = False) -> None:
+    """Route every nn.RMSNorm of ``model`` through FusedRMSNorm (kernels_v3.py:77-83).
+    ``fp16_out``: every norm output of the model feeds only fp16-autocast GEMMs
+    (true of the decoder blocks and the final norm before the tied head)."""
     def forward(self, x):
-        return FusedRMSNorm.apply(x, self.weight, rms_norm_eps(self, x))
+        return FusedRMSNorm.apply(x, self.weight, rms_norm_eps(self, x), fp16_out)
     for module in model.modules():
         if isinstance(module, torch.nn.RMSNorm):
             module.forward = types.MethodType(forward, module)

@@ -23,7 +23,7 @@ import contextlib
 
 import torch
 
-from ._hip import _check, _stream, library
+from ._hip import RV_F16, _check, _stream, library
 
 
 def supported(x: torch.Tensor, up: torch.Tensor, down: torch.Tensor) -> bool:
@@ -126,11 +126,21 @@ def dgate(dy: torch.Tensor, w_down: torch.Tensor, u: torch.Tensor) -> torch.Tens
 
 
 def dx(du: torch.Tensor, w_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out [rows, d] = du W_up rounded to fp16; stored as fp32 (the widened
+    value, for an fp32 input x) or as fp16 (for an fp16 input x)."""
     _f16(du, "du"), _f16(w_up, "W_up")
     rows, two_f = du.shape
     d = w_up.shape[1]
-    _check(library().rv_mlp_dx(du.data_ptr(), w_up.data_ptr(), rows, d, two_f // 2,
-                               out.data_ptr(), _stream(du)), "rv_mlp_dx")
+    if tuple(out.shape) != (rows, d) or not out.is_contiguous():
+        raise ValueError("dx output must be a contiguous [rows, d] tensor")
+    if out.dtype == torch.float32:
+        _check(library().rv_mlp_dx(du.data_ptr(), w_up.data_ptr(), rows, d, two_f // 2,
+                                   out.data_ptr(), _stream(du)), "rv_mlp_dx")
+    elif out.dtype == torch.float16:  # the same contraction as a linear layer's dx
+        _check(library().rv_linear_dx(du.data_ptr(), w_up.data_ptr(), rows, d, two_f,
+                                      out.data_ptr(), RV_F16, _stream(du)), "rv_linear_dx")
+    else:
+        raise ValueError("dx output must be fp32 or fp16")
     return out
 
 

@@ -269,7 +269,10 @@ def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsn
         enable_swiglu(model)
     if rmsnorm:
         from .kernels_v3 import enable_rmsnorm
-        enable_rmsnorm(model)
+        # every norm here feeds only fp16-autocast GEMMs (qkv, the MLP's up
+        # projection, the tied head), so under fp16 autocast it hands them the
+        # fp16 operand directly
+        enable_rmsnorm(model, fp16_out=True)
     model._v3_signature = signature
     return model
 

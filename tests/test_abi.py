@@ -102,3 +102,14 @@ def test_attention_entry_points_validate_without_device():
     assert lib.rv_attn_bwd_workspace_bytes(0, 16, 3) == -2
     assert lib.rv_attn_bwd(fake, fake, fake, fake, 2, 16, 2, 64, fake, fake, 4, None) == 4
     assert lib.rv_attn_bwd(fake, fake, fake, fake, 2, 16, 2, 48, fake, fake, 1 << 20, None) == 3
+
+
+def test_rmsnorm_fp16_entry_points_validate_without_device():
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)
+    assert lib.rv_rmsnorm_fwd_f16(None, fake, fake, fake, 4, 256, 1e-7, None) == 1
+    assert lib.rv_rmsnorm_fwd_f16(fake, fake, fake, fake, 0, 256, 1e-7, None) == 2
+    assert lib.rv_rmsnorm_fwd_f16(fake, fake, fake, fake, 4, 8192, 1e-7, None) == 3
+    assert lib.rv_rmsnorm_fwd_f16(fake, fake, ctypes.c_void_p(4098), fake, 4, 256, 1e-7,
+                                  None) == 3  # fp16 output must be 8-byte aligned
+    assert lib.rv_rmsnorm_bwd_f16(fake, fake, fake, fake, fake, fake, None, 0, 4, 256, None) == 4

@@ -107,6 +107,45 @@ def test_rmsnorm_is_deterministic(cuda_device):
     assert torch.equal(dx1, dx2) and torch.equal(dw1, dw2)
 
 
+@pytest.mark.parametrize("shape", [(14848, 256), (32768, 1024), (7, 100), (3, 4096)])
+def test_rmsnorm_fp16_operand_paths_bitwise(cuda_device, shape):
+    """The fp16-output forward equals the fp32 forward followed by autocast's
+    cast, and the fp16-gradient backward equals the fp32 backward on the same
+    (widened) gradient -- bit for bit."""
+    rows, width = shape
+    g = gen(4)
+    x = torch.randn(rows, width, generator=g).to(cuda_device)
+    w = (1 + 0.02 * torch.randn(width, generator=g)).to(cuda_device)
+    dy16 = torch.randn(rows, width, generator=g).half().to(cuda_device)
+    y32, r32 = ops.rmsnorm_fwd(x, w, EPS32)
+    y16, r16 = ops.rmsnorm_fwd(x, w, EPS32, True)
+    assert y16.dtype == torch.float16 and torch.equal(r16, r32)
+    assert torch.equal(y16, y32.half())
+    dx32, dw32 = ops.rmsnorm_bwd(x, w, dy16.float(), r32)
+    dx16, dw16 = ops.rmsnorm_bwd(x, w, dy16, r32)
+    assert torch.equal(dx16, dx32) and torch.equal(dw16, dw32)
+
+
+def test_fused_rmsnorm_fp16_out_under_autocast(cuda_device):
+    g = gen(5)
+    x = torch.randn(4, 64, 256, generator=g).to(cuda_device).requires_grad_(True)
+    w = torch.ones(256, device=cuda_device, requires_grad=True)
+    lin = (0.05 * torch.randn(512, 256, generator=g)).to(cuda_device)
+    outs = []
+    for flag in (False, True):
+        x.grad = w.grad = None
+        with torch.autocast("cuda", dtype=torch.float16):
+            y = FusedRMSNorm.apply(x, w, EPS32, flag)
+            assert y.dtype == (torch.float16 if flag else torch.float32)
+            z = F.linear(y, lin)
+        z.float().square().sum().backward()
+        outs.append((z.detach(), x.grad.clone(), w.grad.clone()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    # outside autocast the flag changes nothing
+    assert FusedRMSNorm.apply(x.detach(), w.detach(), EPS32, True).dtype == torch.float32
+
+
 def test_rmsnorm_rejects_cpu_and_dtype(cuda_device):
     with pytest.raises(ValueError, match="CUDA FP32"):
         FusedRMSNorm.apply(torch.ones(3, 8, device=cuda_device, dtype=torch.float16),
