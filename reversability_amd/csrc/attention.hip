@@ -16,7 +16,9 @@
 // base 2 (c = scale * log2 e): m = running max of S c, p = 2^(S c - m) in
 // fp32, l = sum p; O^T += V^T P^T on MFMA with P rounded to fp16, so the
 // accumulator holds one query's outputs per lane and the rescale by
-// 2^(m_old - m_new) is lane-local (skipped when no lane's max moved).
+// 2^(m_old - m_new) is lane-local; m moves only when a score exceeds it by
+// more than 2^8, so most tiles skip the rescale.  Tiles the causal diagonal
+// does not cross run a code path without masking.
 // lse = m + log2 l (base-2 units) is kept for the backward.
 //
 // Backward (FA2 order, no atomics, deterministic):
@@ -161,6 +163,100 @@ __device__ __forceinline__ void store4(__half* dst, float a, float b, float c, f
 // ---------------------------------------------------------------------------
 // Forward.
 // ---------------------------------------------------------------------------
+// Value of lane l ^ 32 combined with the lane's own (v_permlane32_swap: the
+// two 32-lane halves exchange; both halves get the same combination, lower
+// half's value first).
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Row of tile element j of a 32 x 32 accumulator, relative to the lane's own
+// first row (l/32)*4: (j/4)*8 + j%4.
+__device__ __forceinline__ constexpr int acc_row(int j) { return (j >> 2) * 8 + (j & 3); }
+
+// The running max is moved only when a score exceeds it by more than kLazy
+// (base-2 units): p = 2^(S c - m) then stays below 2^kLazy (exact in fp16's
+// exponent range), and the rescale of o and l is skipped on most tiles.
+constexpr float kLazy = 8.0f;
+
+template <int HD>
+struct FwdState {
+  f32x16 o[HD / 32];
+  float m, l;
+};
+
+// One 64-key tile for one wave.  MASK: the causal diagonal crosses the tile;
+// key offset (within the tile) k is visible to the lane's query iff
+// k <= rel, rel = q - k0.  live1: the second 32-key half has a visible key
+// for some query of the wave.
+template <int HD, bool MASK>
+__device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, const _Float16* Vs,
+                                         const f16x8 (&qf)[HD / 16], bool live1, int rel,
+                                         float c, int lane) {
+  constexpr int KK = HD / 16, DT = HD / 32;
+  const int hl = lane >> 5;
+  f32x16 s[2];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (sub == 1 && MASK && !live1) break;
+    s[sub] = mfma(frag_row<HD>(Ks, sub * 32 + (lane & 31), 0, hl), qf[0], zero16());
+#pragma unroll
+    for (int kk = 1; kk < KK; ++kk)
+      s[sub] = mfma(frag_row<HD>(Ks, sub * 32 + (lane & 31), kk, hl), qf[kk], s[sub]);
+  }
+  const bool two = !MASK || live1;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (sub == 1 && !two) break;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if constexpr (MASK) {
+        if (sub * 32 + acc_row(j) + hl * 4 > rel) s[sub][j] = -INFINITY;
+      }
+      mx = fmaxf(mx, s[sub][j]);
+    }
+  }
+  const float mxc = pair_max(mx) * c;
+  if (__any(mxc > st.m + kLazy)) {
+    const float m_new = fmaxf(st.m, mxc);
+    const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.m = m_new;
+    st.l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) st.o[dt][e] *= alpha;
+  }
+  const float neg_m = -st.m;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    if (sub == 1 && !two) break;
+    float rowsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(s[sub][j], c, neg_m));
+      rowsum += p;
+      s[sub][j] = p;
+    }
+    st.l += rowsum;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const f16x8 pf = pack8(s[sub], cc);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        st.o[dt] = mfma(frag_tr<HD>(Vs, sub * 32 + cc * 16, dt * 32, lane), pf, st.o[dt]);
+    }
+  }
+}
+
 template <int HD>
 __global__ __launch_bounds__(kThreads, kMinBlocks<HD>)
 void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float* __restrict__ lse,
@@ -184,10 +280,11 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
   for (int kk = 0; kk < KK; ++kk)
     qf[kk] = q < T ? *reinterpret_cast<const f16x8*>(qb + (int64_t)q * rs + kk * 16 + hl * 8)
                    : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
-  f32x16 o[DT];
+  FwdState<HD> st;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = zero16();
-  float m = -INFINITY, l = 0.f;
+  for (int dt = 0; dt < DT; ++dt) st.o[dt] = zero16();
+  st.m = -INFINITY;
+  st.l = 0.f;
 
   const int kv_end = min(T, qt * kBlockRows + kBlockRows);
   const int n_kt = (kv_end + kTile - 1) / kTile;
@@ -206,64 +303,10 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
     }
     const _Float16* Ks = lds[t & 1][0];
     const _Float16* Vs = lds[t & 1][1];
-    if (k0 <= q0 + kWaveRows - 1) {
-      const bool live1 = k0 + 32 <= q0 + kWaveRows - 1;
-      f32x16 s[2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        s[sub] = zero16();
-        if (sub == 0 || live1) {
-#pragma unroll
-          for (int kk = 0; kk < KK; ++kk)
-            s[sub] = mfma(frag_row<HD>(Ks, sub * 32 + (lane & 31), kk, hl), qf[kk], s[sub]);
-        }
-      }
-      const bool diag = k0 + kTile - 1 > q0;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = k0 + sub * 32 + (j >> 2) * 8 + hl * 4 + (j & 3);
-          float v = s[sub][j];
-          if ((sub == 1 && !live1) || (diag && key > q)) v = -INFINITY;
-          s[sub][j] = v;
-          mx = fmaxf(mx, v);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m, mx * c);
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      m = m_new;
-      float rowsum = 0.f;
-      f16x8 pf[2][2];
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(s[sub][j], c, -m_new));
-          rowsum += p;
-          s[sub][j] = p;
-        }
-        pf[sub][0] = pack8(s[sub], 0);
-        pf[sub][1] = pack8(s[sub], 1);
-      }
-      l = l * alpha + rowsum;
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-      }
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        if (sub == 0 || live1) {
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-              o[dt] = mfma(frag_tr<HD>(Vs, sub * 32 + cc * 16, dt * 32, lane), pf[sub][cc], o[dt]);
-        }
-      }
+    if (k0 + kTile - 1 <= q0) {  // every key of the tile precedes every query of the wave
+      fwd_tile<HD, false>(st, Ks, Vs, qf, true, 0, c, lane);
+    } else if (k0 <= q0 + kWaveRows - 1) {  // the diagonal crosses the tile
+      fwd_tile<HD, true>(st, Ks, Vs, qf, k0 + 32 <= q0 + kWaveRows - 1, q - k0, c, lane);
     }
     if (more) {
       ck.store(lds[(t + 1) & 1][0]);
@@ -271,7 +314,7 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
     }
     __syncthreads();
   }
-  l += __shfl_xor(l, 32);
+  const float l = pair_sum(st.l);
   if (q < T) {
     const float inv = 1.0f / l;
     __half* orow = out + ((int64_t)b * T + q) * H * HD + (int64_t)h * HD;
@@ -279,9 +322,10 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int jg = 0; jg < 4; ++jg)
-        store4(orow + dt * 32 + jg * 8 + hl * 4, o[dt][4 * jg] * inv, o[dt][4 * jg + 1] * inv,
-               o[dt][4 * jg + 2] * inv, o[dt][4 * jg + 3] * inv);
-    if (hl == 0) lse[(int64_t)bh * T + q] = m + __log2f(l);
+        store4(orow + dt * 32 + jg * 8 + hl * 4, st.o[dt][4 * jg] * inv,
+               st.o[dt][4 * jg + 1] * inv, st.o[dt][4 * jg + 2] * inv,
+               st.o[dt][4 * jg + 3] * inv);
+    if (hl == 0) lse[(int64_t)bh * T + q] = st.m + __log2f(l);
   }
 }
 
@@ -309,6 +353,90 @@ void attn_bwd_pre_k(const __half* __restrict__ out, const __half* __restrict__ d
   const int h = (int)(r % H);
   const int64_t b = bt / T, t = bt % T;
   delta[(b * H + h) * T + t] = acc;
+}
+
+// dK/dV contribution of 32 staged queries (tile rows r0 .. r0 + 31 of Q / dO)
+// to one wave's 32 keys (lanes).  MASK: the causal diagonal crosses the pair;
+// tile row r is visible to the lane's key iff r >= krel = key - (first query
+// of the tile).  Query rows past the sequence hold zeros (Q, dO, lse, delta):
+// their P is 1 but dS = 0 and dO = 0, so they add nothing.
+template <int HD, bool MASK>
+__device__ __forceinline__ void kv_rows(f32x16 (&dk)[HD / 32], f32x16 (&dv)[HD / 32],
+                                        const _Float16* Qs, const _Float16* Gs, const float* Ls,
+                                        const float* Ds, const f16x8 (&kf)[HD / 16],
+                                        const f16x8 (&vf)[HD / 16], int r0, int krel, float c,
+                                        int lane) {
+  constexpr int KK = HD / 16, DT = HD / 32;
+  const int hl = lane >> 5;
+  f32x16 s = mfma(frag_row<HD>(Qs, r0 + (lane & 31), 0, hl), kf[0], zero16());
+  f32x16 dp = mfma(frag_row<HD>(Gs, r0 + (lane & 31), 0, hl), vf[0], zero16());
+#pragma unroll
+  for (int kk = 1; kk < KK; ++kk) {
+    s = mfma(frag_row<HD>(Qs, r0 + (lane & 31), kk, hl), kf[kk], s);
+    dp = mfma(frag_row<HD>(Gs, r0 + (lane & 31), kk, hl), vf[kk], dp);
+  }
+#pragma unroll
+  for (int jg = 0; jg < 4; ++jg) {
+    const int r4 = r0 + jg * 8 + hl * 4;
+    const float4 L4 = *reinterpret_cast<const float4*>(Ls + r4);
+    const float4 D4 = *reinterpret_cast<const float4*>(Ds + r4);
+    const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
+    const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 4 * jg + e;
+      float p = __builtin_amdgcn_exp2f(fmaf(s[j], c, -Lr[e]));
+      if constexpr (MASK) {
+        if (r4 + e < krel) p = 0.f;
+      }
+      s[j] = p;
+      dp[j] = p * (dp[j] - Dr[e]);
+    }
+  }
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    const f16x8 pf = pack8(s, cc), dsf = pack8(dp, cc);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      dv[dt] = mfma(frag_tr<HD>(Gs, r0 + cc * 16, dt * 32, lane), pf, dv[dt]);
+      dk[dt] = mfma(frag_tr<HD>(Qs, r0 + cc * 16, dt * 32, lane), dsf, dk[dt]);
+    }
+  }
+}
+
+// dQ contribution of 32 staged keys (tile rows r0 .. r0 + 31 of K / V) to one
+// wave's 32 queries (lanes).  MASK: tile row r is visible iff r <= qrel =
+// query - (first key of the tile).
+template <int HD, bool MASK>
+__device__ __forceinline__ void q_rows(f32x16 (&dq)[HD / 32], const _Float16* Ks,
+                                       const _Float16* Vs, const f16x8 (&qf)[HD / 16],
+                                       const f16x8 (&gf)[HD / 16], float Lq, float Dq, int r0,
+                                       int qrel, float c, int lane) {
+  constexpr int KK = HD / 16, DT = HD / 32;
+  const int hl = lane >> 5;
+  f32x16 s = mfma(frag_row<HD>(Ks, r0 + (lane & 31), 0, hl), qf[0], zero16());
+  f32x16 dp = mfma(frag_row<HD>(Vs, r0 + (lane & 31), 0, hl), gf[0], zero16());
+#pragma unroll
+  for (int kk = 1; kk < KK; ++kk) {
+    s = mfma(frag_row<HD>(Ks, r0 + (lane & 31), kk, hl), qf[kk], s);
+    dp = mfma(frag_row<HD>(Vs, r0 + (lane & 31), kk, hl), gf[kk], dp);
+  }
+  const float neg_l = -Lq;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float p = __builtin_amdgcn_exp2f(fmaf(s[j], c, neg_l));
+    if constexpr (MASK) {
+      if (r0 + acc_row(j) + hl * 4 > qrel) p = 0.f;
+    }
+    dp[j] = p * (dp[j] - Dq);
+  }
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    const f16x8 dsf = pack8(dp, cc);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      dq[dt] = mfma(frag_tr<HD>(Ks, r0 + cc * 16, dt * 32, lane), dsf, dq[dt]);
+  }
 }
 
 template <int HD>
@@ -376,45 +504,14 @@ void attn_bwd_kv_k(const __half* __restrict__ qkv, const __half* __restrict__ do
     const _Float16* Gs = lds[t & 1][1];
     const float* Ls = rowv[t & 1][0];
     const float* Ds = rowv[t & 1][1];
-    if (qt0 + kTile - 1 >= k0w) {
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int qs = qt0 + sub * 32;
-        if (qs + 31 < k0w) continue;  // every query of this half precedes every key
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          s = mfma(frag_row<HD>(Qs, sub * 32 + (lane & 31), kk, hl), kf[kk], s);
-          dp = mfma(frag_row<HD>(Gs, sub * 32 + (lane & 31), kk, hl), vf[kk], dp);
-        }
-        const bool diag = qs < k0w + kWaveRows - 1;
-#pragma unroll
-        for (int jg = 0; jg < 4; ++jg) {
-          const int r4 = sub * 32 + jg * 8 + hl * 4;
-          const float4 L4 = *reinterpret_cast<const float4*>(Ls + r4);
-          const float4 D4 = *reinterpret_cast<const float4*>(Ds + r4);
-          const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
-          const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = 4 * jg + e;
-            const int query = qt0 + r4 + e;
-            float p = __builtin_amdgcn_exp2f(fmaf(s[j], c, -Lr[e]));
-            if ((diag && key > query) || query >= T) p = 0.f;
-            s[j] = p;
-            dp[j] = p * (dp[j] - Dr[e]);
-          }
-        }
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const f16x8 pf = pack8(s, cc), dsf = pack8(dp, cc);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            dv[dt] = mfma(frag_tr<HD>(Gs, sub * 32 + cc * 16, dt * 32, lane), pf, dv[dt]);
-            dk[dt] = mfma(frag_tr<HD>(Qs, sub * 32 + cc * 16, dt * 32, lane), dsf, dk[dt]);
-          }
-        }
-      }
+    for (int sub = 0; sub < 2; ++sub) {
+      const int qs = qt0 + sub * 32;
+      if (qs + kWaveRows - 1 < k0w) continue;  // every query of the half precedes every key
+      if (qs >= k0w + kWaveRows - 1)
+        kv_rows<HD, false>(dk, dv, Qs, Gs, Ls, Ds, kf, vf, sub * 32, 0, c, lane);
+      else
+        kv_rows<HD, true>(dk, dv, Qs, Gs, Ls, Ds, kf, vf, sub * 32, key - qt0, c, lane);
     }
     if (more) {
       cq.store(lds[(t + 1) & 1][0]);
@@ -494,33 +591,14 @@ void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ dou
     }
     const _Float16* Ks = lds[t & 1][0];
     const _Float16* Vs = lds[t & 1][1];
-    if (k0 <= q0 + kWaveRows - 1) {
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int ks = k0 + sub * 32;
-        if (ks > q0 + kWaveRows - 1) continue;  // every key of this half follows every query
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          s = mfma(frag_row<HD>(Ks, sub * 32 + (lane & 31), kk, hl), qf[kk], s);
-          dp = mfma(frag_row<HD>(Vs, sub * 32 + (lane & 31), kk, hl), gf[kk], dp);
-        }
-        const bool diag = ks + 31 > q0;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int keyj = ks + (j >> 2) * 8 + hl * 4 + (j & 3);
-          float p = __builtin_amdgcn_exp2f(fmaf(s[j], c, -Lq));
-          if (diag && keyj > q) p = 0.f;
-          dp[j] = p * (dp[j] - Dq);
-        }
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const f16x8 dsf = pack8(dp, cc);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            dq[dt] = mfma(frag_tr<HD>(Ks, sub * 32 + cc * 16, dt * 32, lane), dsf, dq[dt]);
-        }
-      }
+    for (int sub = 0; sub < 2; ++sub) {
+      const int ks = k0 + sub * 32;
+      if (ks > q0 + kWaveRows - 1) continue;  // every key of the half follows every query
+      if (ks + kWaveRows - 1 <= q0)
+        q_rows<HD, false>(dq, Ks, Vs, qf, gf, Lq, Dq, sub * 32, 0, c, lane);
+      else
+        q_rows<HD, true>(dq, Ks, Vs, qf, gf, Lq, Dq, sub * 32, q - k0, c, lane);
     }
     if (more) {
       ck.store(lds[(t + 1) & 1][0]);
