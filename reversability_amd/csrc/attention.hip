@@ -66,6 +66,9 @@ constexpr int kTile = 64;        // rows per streamed LDS tile
 // for HD = 128, whose accumulators need the whole 512-register file.
 template <int HD>
 constexpr int kMinBlocks = HD == 128 ? 1 : 2;
+// The forward keeps fewer live registers: three workgroups per CU at HD = 64.
+template <int HD>
+constexpr int kFwdMinBlocks = HD == 128 ? 1 : (HD == 64 ? 3 : 2);
 
 template <int HD>
 __device__ __forceinline__ int swz(int r, int c) {
@@ -192,24 +195,59 @@ struct FwdState {
   float m, l;
 };
 
+// A lane's LDS offsets (halves) inside one [64][HD] tile, fixed for the whole
+// kernel: row operands of rows 0..31 (rows 32..63 add 32 HD: the swizzle
+// depends on the row's low five bits only) and transposed operands of the
+// rows sigma of each 16-row group, upper half of each read pair included.
+template <int HD>
+struct FragOffsets {
+  int row[HD / 16];           // frag_row(t, lane % 32, kk, hl)
+  int tr[2][HD / 32][2];      // frag_tr(t, cc * 16, dt * 32, lane): [cc][dt][first / second]
+  __device__ __forceinline__ explicit FragOffsets(int lane) {
+    const int hl = lane >> 5, g = lane >> 4, i = lane & 15;
+#pragma unroll
+    for (int kk = 0; kk < HD / 16; ++kk)
+      row[kk] = (lane & 31) * HD + (swz<HD>(lane & 31, kk * 2 + hl) << 3);
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int dt = 0; dt < HD / 32; ++dt) {
+        const int r = cc * 16 + (g >> 1) * 4 + (i >> 2);
+        const int col = dt * 32 + (g & 1) * 16 + 4 * (i & 3);
+        tr[cc][dt][0] = lds_at<HD>(r, col);
+        tr[cc][dt][1] = lds_at<HD>(r + 8, col);
+      }
+  }
+  __device__ __forceinline__ f16x8 rowf(const _Float16* t, int sub, int kk) const {
+    return *reinterpret_cast<const f16x8*>(t + sub * 32 * HD + row[kk]);
+  }
+  __device__ __forceinline__ f16x8 trf(const _Float16* t, int sub, int cc, int dt) const {
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (RV_LDS i16x4*)(t + sub * 32 * HD + tr[cc][dt][0]));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (RV_LDS i16x4*)(t + sub * 32 * HD + tr[cc][dt][1]));
+    const f16x4 a = __builtin_bit_cast(f16x4, lo), b = __builtin_bit_cast(f16x4, hi);
+    return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  }
+};
+
 // One 64-key tile for one wave.  MASK: the causal diagonal crosses the tile;
 // key offset (within the tile) k is visible to the lane's query iff
 // k <= rel, rel = q - k0.  live1: the second 32-key half has a visible key
 // for some query of the wave.
 template <int HD, bool MASK>
 __device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, const _Float16* Vs,
-                                         const f16x8 (&qf)[HD / 16], bool live1, int rel,
-                                         float c, int lane) {
+                                         const FragOffsets<HD>& fo, const f16x8 (&qf)[HD / 16],
+                                         bool live1, int rel, float c, int lane) {
   constexpr int KK = HD / 16, DT = HD / 32;
   const int hl = lane >> 5;
   f32x16 s[2];
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     if (sub == 1 && MASK && !live1) break;
-    s[sub] = mfma(frag_row<HD>(Ks, sub * 32 + (lane & 31), 0, hl), qf[0], zero16());
+    s[sub] = mfma(fo.rowf(Ks, sub, 0), qf[0], zero16());
 #pragma unroll
-    for (int kk = 1; kk < KK; ++kk)
-      s[sub] = mfma(frag_row<HD>(Ks, sub * 32 + (lane & 31), kk, hl), qf[kk], s[sub]);
+    for (int kk = 1; kk < KK; ++kk) s[sub] = mfma(fo.rowf(Ks, sub, kk), qf[kk], s[sub]);
   }
   const bool two = !MASK || live1;
   float mx = -INFINITY;
@@ -251,14 +289,13 @@ __device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, c
     for (int cc = 0; cc < 2; ++cc) {
       const f16x8 pf = pack8(s[sub], cc);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        st.o[dt] = mfma(frag_tr<HD>(Vs, sub * 32 + cc * 16, dt * 32, lane), pf, st.o[dt]);
+      for (int dt = 0; dt < DT; ++dt) st.o[dt] = mfma(fo.trf(Vs, sub, cc, dt), pf, st.o[dt]);
     }
   }
 }
 
 template <int HD>
-__global__ __launch_bounds__(kThreads, kMinBlocks<HD>)
+__global__ __launch_bounds__(kThreads, kFwdMinBlocks<HD>)
 void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float* __restrict__ lse,
                 int T, int H, int n_qt, float c) {
   constexpr int KK = HD / 16, DT = HD / 32;
@@ -274,6 +311,7 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
   const __half* vb = qb + (int64_t)2 * H * HD;
   const int q0 = qt * kBlockRows + wave * kWaveRows;
   const int q = q0 + (lane & 31);
+  const FragOffsets<HD> fo(lane);
 
   f16x8 qf[KK];
 #pragma unroll
@@ -294,26 +332,33 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
   ck.store(lds[0][0]);
   cv.store(lds[0][1]);
   __syncthreads();
-  for (int t = 0; t < n_kt; ++t) {
-    const int k0 = t * kTile;
-    const bool more = t + 1 < n_kt;
-    if (more) {
-      ck.load(kb, rs, k0 + kTile, T);
-      cv.load(vb, rs, k0 + kTile, T);
-    }
-    const _Float16* Ks = lds[t & 1][0];
-    const _Float16* Vs = lds[t & 1][1];
-    if (k0 + kTile - 1 <= q0) {  // every key of the tile precedes every query of the wave
-      fwd_tile<HD, false>(st, Ks, Vs, qf, true, 0, c, lane);
-    } else if (k0 <= q0 + kWaveRows - 1) {  // the diagonal crosses the tile
-      fwd_tile<HD, true>(st, Ks, Vs, qf, k0 + 32 <= q0 + kWaveRows - 1, q - k0, c, lane);
-    }
-    if (more) {
-      ck.store(lds[(t + 1) & 1][0]);
-      cv.store(lds[(t + 1) & 1][1]);
-    }
-    __syncthreads();
+  // Tile t lives in buffer t % 2; the loop body is written out for both
+  // buffers so that each buffer's LDS address is a constant.
+#define RV_FWD_STEP(BUF)                                                                    \
+  {                                                                                         \
+    const int k0 = t * kTile;                                                               \
+    const bool more = t + 1 < n_kt;                                                         \
+    if (more) {                                                                             \
+      ck.load(kb, rs, k0 + kTile, T);                                                       \
+      cv.load(vb, rs, k0 + kTile, T);                                                       \
+    }                                                                                       \
+    if (k0 + kTile - 1 <= q0)                                                               \
+      fwd_tile<HD, false>(st, lds[BUF][0], lds[BUF][1], fo, qf, true, 0, c, lane);          \
+    else if (k0 <= q0 + kWaveRows - 1)                                                      \
+      fwd_tile<HD, true>(st, lds[BUF][0], lds[BUF][1], fo, qf,                              \
+                         k0 + 32 <= q0 + kWaveRows - 1, q - k0, c, lane);                    \
+    if (more) {                                                                             \
+      ck.store(lds[1 - (BUF)][0]);                                                          \
+      cv.store(lds[1 - (BUF)][1]);                                                          \
+    }                                                                                       \
+    __syncthreads();                                                                        \
   }
+  for (int t = 0; t < n_kt; ++t) {
+    RV_FWD_STEP(0)
+    if (++t >= n_kt) break;
+    RV_FWD_STEP(1)
+  }
+#undef RV_FWD_STEP
   const float l = pair_sum(st.l);
   if (q < T) {
     const float inv = 1.0f / l;
