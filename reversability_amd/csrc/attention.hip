@@ -94,26 +94,6 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
-// Row operand: 8 halves of tile row r at columns kk*16 + hl*8.
-template <int HD>
-__device__ __forceinline__ f16x8 frag_row(const _Float16* t, int r, int kk, int hl) {
-  return *reinterpret_cast<const f16x8*>(t + r * HD + (swz<HD>(r, kk * 2 + hl) << 3));
-}
-
-// Transposed operand: lane l supplies tile column col0 + l % 32 at the tile
-// rows sigma: rbase + (l/32)*4 + 0..3, then rbase + 8 + (l/32)*4 + 0..3.
-template <int HD>
-__device__ __forceinline__ f16x8 frag_tr(const _Float16* t, int rbase, int col0, int lane) {
-  const int g = lane >> 4, i = lane & 15;
-  const int r = rbase + (g >> 1) * 4 + (i >> 2);
-  const int col = col0 + (g & 1) * 16 + 4 * (i & 3);
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((RV_LDS i16x4*)(t + lds_at<HD>(r, col)));
-  const i16x4 hi =
-      __builtin_amdgcn_ds_read_tr16_b64_v4i16((RV_LDS i16x4*)(t + lds_at<HD>(r + 8, col)));
-  const f16x4 a = __builtin_bit_cast(f16x4, lo), b = __builtin_bit_cast(f16x4, hi);
-  return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-
 // Values 8 h .. 8 h + 7 of an accumulator as an fp16 operand.
 __device__ __forceinline__ f16x8 pack8(const f32x16& v, int h) {
   f16x8 r;
@@ -408,17 +388,19 @@ void attn_bwd_pre_k(const __half* __restrict__ out, const __half* __restrict__ d
 template <int HD, bool MASK>
 __device__ __forceinline__ void kv_rows(f32x16 (&dk)[HD / 32], f32x16 (&dv)[HD / 32],
                                         const _Float16* Qs, const _Float16* Gs, const float* Ls,
-                                        const float* Ds, const f16x8 (&kf)[HD / 16],
+                                        const float* Ds, const FragOffsets<HD>& fo,
+                                        const f16x8 (&kf)[HD / 16],
                                         const f16x8 (&vf)[HD / 16], int r0, int krel, float c,
                                         int lane) {
   constexpr int KK = HD / 16, DT = HD / 32;
   const int hl = lane >> 5;
-  f32x16 s = mfma(frag_row<HD>(Qs, r0 + (lane & 31), 0, hl), kf[0], zero16());
-  f32x16 dp = mfma(frag_row<HD>(Gs, r0 + (lane & 31), 0, hl), vf[0], zero16());
+  const int sub = r0 / 32;
+  f32x16 s = mfma(fo.rowf(Qs, sub, 0), kf[0], zero16());
+  f32x16 dp = mfma(fo.rowf(Gs, sub, 0), vf[0], zero16());
 #pragma unroll
   for (int kk = 1; kk < KK; ++kk) {
-    s = mfma(frag_row<HD>(Qs, r0 + (lane & 31), kk, hl), kf[kk], s);
-    dp = mfma(frag_row<HD>(Gs, r0 + (lane & 31), kk, hl), vf[kk], dp);
+    s = mfma(fo.rowf(Qs, sub, kk), kf[kk], s);
+    dp = mfma(fo.rowf(Gs, sub, kk), vf[kk], dp);
   }
 #pragma unroll
   for (int jg = 0; jg < 4; ++jg) {
@@ -443,8 +425,8 @@ __device__ __forceinline__ void kv_rows(f32x16 (&dk)[HD / 32], f32x16 (&dv)[HD /
     const f16x8 pf = pack8(s, cc), dsf = pack8(dp, cc);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      dv[dt] = mfma(frag_tr<HD>(Gs, r0 + cc * 16, dt * 32, lane), pf, dv[dt]);
-      dk[dt] = mfma(frag_tr<HD>(Qs, r0 + cc * 16, dt * 32, lane), dsf, dk[dt]);
+      dv[dt] = mfma(fo.trf(Gs, sub, cc, dt), pf, dv[dt]);
+      dk[dt] = mfma(fo.trf(Qs, sub, cc, dt), dsf, dk[dt]);
     }
   }
 }
@@ -454,17 +436,19 @@ __device__ __forceinline__ void kv_rows(f32x16 (&dk)[HD / 32], f32x16 (&dv)[HD /
 // query - (first key of the tile).
 template <int HD, bool MASK>
 __device__ __forceinline__ void q_rows(f32x16 (&dq)[HD / 32], const _Float16* Ks,
-                                       const _Float16* Vs, const f16x8 (&qf)[HD / 16],
+                                       const _Float16* Vs, const FragOffsets<HD>& fo,
+                                       const f16x8 (&qf)[HD / 16],
                                        const f16x8 (&gf)[HD / 16], float Lq, float Dq, int r0,
                                        int qrel, float c, int lane) {
   constexpr int KK = HD / 16, DT = HD / 32;
   const int hl = lane >> 5;
-  f32x16 s = mfma(frag_row<HD>(Ks, r0 + (lane & 31), 0, hl), qf[0], zero16());
-  f32x16 dp = mfma(frag_row<HD>(Vs, r0 + (lane & 31), 0, hl), gf[0], zero16());
+  const int sub = r0 / 32;
+  f32x16 s = mfma(fo.rowf(Ks, sub, 0), qf[0], zero16());
+  f32x16 dp = mfma(fo.rowf(Vs, sub, 0), gf[0], zero16());
 #pragma unroll
   for (int kk = 1; kk < KK; ++kk) {
-    s = mfma(frag_row<HD>(Ks, r0 + (lane & 31), kk, hl), qf[kk], s);
-    dp = mfma(frag_row<HD>(Vs, r0 + (lane & 31), kk, hl), gf[kk], dp);
+    s = mfma(fo.rowf(Ks, sub, kk), qf[kk], s);
+    dp = mfma(fo.rowf(Vs, sub, kk), gf[kk], dp);
   }
   const float neg_l = -Lq;
 #pragma unroll
@@ -480,7 +464,7 @@ __device__ __forceinline__ void q_rows(f32x16 (&dq)[HD / 32], const _Float16* Ks
     const f16x8 dsf = pack8(dp, cc);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      dq[dt] = mfma(frag_tr<HD>(Ks, r0 + cc * 16, dt * 32, lane), dsf, dq[dt]);
+      dq[dt] = mfma(fo.trf(Ks, sub, cc, dt), dsf, dq[dt]);
   }
 }
 
@@ -536,38 +520,43 @@ void attn_bwd_kv_k(const __half* __restrict__ qkv, const __half* __restrict__ do
     rowv[0][1][threadIdx.x] = dvv;
   }
   __syncthreads();
-  for (int t = 0; t < n_qtiles; ++t) {
-    const int qt0 = kbase + t * kTile;
-    const bool more = t + 1 < n_qtiles;
-    if (more) {
-      cq.load(qb, rs, qt0 + kTile, T);
-      cg.load(gb, os, qt0 + kTile, T);
-      lv = load_rowval(lb, qt0 + kTile, T);
-      dvv = load_rowval(db, qt0 + kTile, T);
-    }
-    const _Float16* Qs = lds[t & 1][0];
-    const _Float16* Gs = lds[t & 1][1];
-    const float* Ls = rowv[t & 1][0];
-    const float* Ds = rowv[t & 1][1];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int qs = qt0 + sub * 32;
-      if (qs + kWaveRows - 1 < k0w) continue;  // every query of the half precedes every key
-      if (qs >= k0w + kWaveRows - 1)
-        kv_rows<HD, false>(dk, dv, Qs, Gs, Ls, Ds, kf, vf, sub * 32, 0, c, lane);
-      else
-        kv_rows<HD, true>(dk, dv, Qs, Gs, Ls, Ds, kf, vf, sub * 32, key - qt0, c, lane);
-    }
-    if (more) {
-      cq.store(lds[(t + 1) & 1][0]);
-      cg.store(lds[(t + 1) & 1][1]);
-      if (threadIdx.x < kTile) {
-        rowv[(t + 1) & 1][0][threadIdx.x] = lv;
-        rowv[(t + 1) & 1][1][threadIdx.x] = dvv;
-      }
-    }
-    __syncthreads();
+  const FragOffsets<HD> fo(lane);
+#define RV_KV_STEP(BUF)                                                                     \
+  {                                                                                         \
+    const int qt0 = kbase + t * kTile;                                                      \
+    const bool more = t + 1 < n_qtiles;                                                     \
+    if (more) {                                                                             \
+      cq.load(qb, rs, qt0 + kTile, T);                                                      \
+      cg.load(gb, os, qt0 + kTile, T);                                                      \
+      lv = load_rowval(lb, qt0 + kTile, T);                                                 \
+      dvv = load_rowval(db, qt0 + kTile, T);                                                \
+    }                                                                                       \
+    _Pragma("unroll") for (int sub = 0; sub < 2; ++sub) {                                   \
+      const int qs = qt0 + sub * 32;                                                        \
+      if (qs + kWaveRows - 1 < k0w) continue; /* every query precedes every key */          \
+      if (qs >= k0w + kWaveRows - 1)                                                        \
+        kv_rows<HD, false>(dk, dv, lds[BUF][0], lds[BUF][1], rowv[BUF][0], rowv[BUF][1], fo, \
+                           kf, vf, sub * 32, 0, c, lane);                                   \
+      else                                                                                  \
+        kv_rows<HD, true>(dk, dv, lds[BUF][0], lds[BUF][1], rowv[BUF][0], rowv[BUF][1], fo,  \
+                          kf, vf, sub * 32, key - qt0, c, lane);                            \
+    }                                                                                       \
+    if (more) {                                                                             \
+      cq.store(lds[1 - (BUF)][0]);                                                          \
+      cg.store(lds[1 - (BUF)][1]);                                                          \
+      if (threadIdx.x < kTile) {                                                            \
+        rowv[1 - (BUF)][0][threadIdx.x] = lv;                                               \
+        rowv[1 - (BUF)][1][threadIdx.x] = dvv;                                              \
+      }                                                                                     \
+    }                                                                                       \
+    __syncthreads();                                                                        \
   }
+  for (int t = 0; t < n_qtiles; ++t) {
+    RV_KV_STEP(0)
+    if (++t >= n_qtiles) break;
+    RV_KV_STEP(1)
+  }
+#undef RV_KV_STEP
   if (key < T) {
     __half* krow = dqkv + ((int64_t)b * T + key) * rs + os + (int64_t)h * HD;
     __half* vrow = krow + os;
@@ -627,30 +616,37 @@ void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ dou
   ck.store(lds[0][0]);
   cv.store(lds[0][1]);
   __syncthreads();
-  for (int t = 0; t < n_kt; ++t) {
-    const int k0 = t * kTile;
-    const bool more = t + 1 < n_kt;
-    if (more) {
-      ck.load(kb, rs, k0 + kTile, T);
-      cv.load(vb, rs, k0 + kTile, T);
-    }
-    const _Float16* Ks = lds[t & 1][0];
-    const _Float16* Vs = lds[t & 1][1];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int ks = k0 + sub * 32;
-      if (ks > q0 + kWaveRows - 1) continue;  // every key of the half follows every query
-      if (ks + kWaveRows - 1 <= q0)
-        q_rows<HD, false>(dq, Ks, Vs, qf, gf, Lq, Dq, sub * 32, 0, c, lane);
-      else
-        q_rows<HD, true>(dq, Ks, Vs, qf, gf, Lq, Dq, sub * 32, q - k0, c, lane);
-    }
-    if (more) {
-      ck.store(lds[(t + 1) & 1][0]);
-      cv.store(lds[(t + 1) & 1][1]);
-    }
-    __syncthreads();
+  const FragOffsets<HD> fo(lane);
+#define RV_Q_STEP(BUF)                                                                      \
+  {                                                                                         \
+    const int k0 = t * kTile;                                                               \
+    const bool more = t + 1 < n_kt;                                                         \
+    if (more) {                                                                             \
+      ck.load(kb, rs, k0 + kTile, T);                                                       \
+      cv.load(vb, rs, k0 + kTile, T);                                                       \
+    }                                                                                       \
+    _Pragma("unroll") for (int sub = 0; sub < 2; ++sub) {                                   \
+      const int ks = k0 + sub * 32;                                                         \
+      if (ks > q0 + kWaveRows - 1) continue; /* every key follows every query */            \
+      if (ks + kWaveRows - 1 <= q0)                                                         \
+        q_rows<HD, false>(dq, lds[BUF][0], lds[BUF][1], fo, qf, gf, Lq, Dq, sub * 32, 0, c, \
+                          lane);                                                            \
+      else                                                                                  \
+        q_rows<HD, true>(dq, lds[BUF][0], lds[BUF][1], fo, qf, gf, Lq, Dq, sub * 32, q - k0, \
+                         c, lane);                                                          \
+    }                                                                                       \
+    if (more) {                                                                             \
+      ck.store(lds[1 - (BUF)][0]);                                                          \
+      cv.store(lds[1 - (BUF)][1]);                                                          \
+    }                                                                                       \
+    __syncthreads();                                                                        \
   }
+  for (int t = 0; t < n_kt; ++t) {
+    RV_Q_STEP(0)
+    if (++t >= n_kt) break;
+    RV_Q_STEP(1)
+  }
+#undef RV_Q_STEP
   if (qok) {
     __half* qrow = dqkv + ((int64_t)b * T + q) * rs + (int64_t)h * HD;
 #pragma unroll
