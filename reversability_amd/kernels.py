@@ -60,6 +60,64 @@ def cross_entropy_sum(logits, labels):
     return TiledCrossEntropy.apply(logits, labels)
 
 
+VOCAB_ALIGN = 64  # padded logits row stride (in elements) of tied_head_ce
+
+
+def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: torch.Tensor,
+                 grad: torch.Tensor):
+    """One chunk of the tied head and its summed cross-entropy, forward and
+    backward, with the logits stored at a padded row stride.
+
+    The same computation as ``cross_entropy_sum(F.linear(x16, head16[:vocab]),
+    labels)`` under fp16 autocast followed by its backward with upstream
+    gradient ``grad`` (a device fp32 scalar): logits = fp16(x16 W^T); loss and
+    dlogits from the fused cross-entropy kernels; dx = dlogits W and
+    dW = dlogits^T x16 (fp16, as autocast's linear produces them).  ``head16`` is
+    the fp16 head with its rows padded to a multiple of VOCAB_ALIGN (the pad
+    rows zero), so every logits row starts 16-byte aligned: with the odd
+    vocabulary (50257) as the row stride, hipBLASLt's GEMMs over the logits
+    run 15-25% slower on MI355X.  Returns (loss sum, dx16, dW16 [vocab, d]).
+    """
+    rows, d = x16.shape
+    padded = head16.shape[0]
+    if (x16.dtype != torch.float16 or head16.dtype != torch.float16 or not x16.is_contiguous()
+            or not head16.is_contiguous() or head16.shape[1] != d or padded % VOCAB_ALIGN
+            or not 0 < vocab <= padded or labels.dtype != torch.int64
+            or labels.numel() != rows or not x16.is_cuda):
+        raise ValueError("tied_head_ce needs contiguous CUDA fp16 x [rows, d], a padded fp16 "
+                         "head [padded, d] and int64 labels [rows]")
+    from ._hip import RV_F16, _check, _stream, library
+    lib = library()
+    labels = labels.contiguous()
+    logits = torch.mm(x16, head16.t())                       # [rows, padded] fp16
+    rmax, rlse, losses = (torch.empty(rows, device=x16.device, dtype=torch.float32)
+                          for _ in range(3))
+    dlogits = torch.empty_like(logits)
+    st = _stream(x16)
+    if rows:
+        _check(lib.rv_ce_fwd(logits.data_ptr(), RV_F16, padded, labels.data_ptr(), rows, vocab,
+                             IGNORE_INDEX, rmax.data_ptr(), rlse.data_ptr(), losses.data_ptr(),
+                             st), "rv_ce_fwd")
+        _check(lib.rv_ce_bwd(logits.data_ptr(), RV_F16, padded, labels.data_ptr(),
+                             rmax.data_ptr(), rlse.data_ptr(), grad.data_ptr(), rows, vocab,
+                             IGNORE_INDEX, dlogits.data_ptr(), st), "rv_ce_bwd")
+    del logits
+    d_view = dlogits[:, :vocab]
+    dx16 = torch.mm(d_view, head16[:vocab])
+    dw16 = torch.mm(d_view.t(), x16)
+    return losses.sum(), dx16, dw16
+
+
+def padded_head(weight: torch.Tensor) -> torch.Tensor:
+    """fp16 copy of a [vocab, d] head with zero rows up to a multiple of VOCAB_ALIGN."""
+    vocab, d = weight.shape
+    padded = -(-vocab // VOCAB_ALIGN) * VOCAB_ALIGN
+    head = torch.empty(padded, d, device=weight.device, dtype=torch.float16)
+    head[:vocab].copy_(weight)
+    head[vocab:].zero_()
+    return head
+
+
 def _validate(up: torch.Tensor) -> None:
     # kernels.py:116-117
     if (up.device.type != "cuda" or up.dtype not in (torch.float16, torch.float32)

@@ -238,6 +238,44 @@ class SplitMidpoint(torch.autograd.Function):
         return (dp, dq, None, None, *grads)
 
 
+def _fused_head(hidden, weight, labels, denominator, chunk_tokens, scaler, precision, device):
+    """The chunk loop of cached_head_backward for the fused fp16 loss, without
+    building an autograd graph for the head: per chunk the fp16 logits (padded
+    row stride), the fused cross-entropy forward and backward with the upstream
+    gradient d(scale * loss / denominator)/d loss = scale / denominator, and
+    the two gradient GEMMs (kernels.tied_head_ce).  Same values as the autograd
+    loop: the head's fp16 gradient of each chunk is widened and added to the
+    tied weight's gradient, the hidden-state gradient of each chunk fills its
+    rows, and one core backward follows."""
+    from .kernels import padded_head, tied_head_ce
+    flat = hidden.detach().reshape(-1, hidden.shape[-1])
+    x16 = flat if flat.dtype == torch.float16 else flat.to(torch.float16)
+    x16 = x16.contiguous()
+    head16 = padded_head(weight.detach())
+    vocab = weight.shape[0]
+    one = torch.ones((), device=device, dtype=torch.float32)
+    grad = (one if scaler is None else scaler.scale(one)) / denominator
+    targets = labels.reshape(-1)
+    dflat = torch.empty_like(flat)
+    total = torch.zeros((), device=device, dtype=torch.float32)
+    for start in range(0, targets.numel(), chunk_tokens):
+        stop = start + chunk_tokens
+        loss, dx16, dw16 = tied_head_ce(x16[start:stop], head16, vocab, targets[start:stop],
+                                        grad.reshape(1))
+        dflat[start:stop].copy_(dx16)
+        chunk_grad = dw16.to(weight.dtype)
+        if weight.grad is None:
+            weight.grad = chunk_grad
+        else:
+            weight.grad.add_(chunk_grad)
+        total += loss.detach().float()
+        del dx16, dw16, chunk_grad
+    del head16, x16
+    with amp_context(device, precision):
+        hidden.backward(dflat.reshape_as(hidden))
+    return total
+
+
 def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsnorm=False):
     """Wire the optimized core, tiled MLP, fused SwiGLU and fused RMSNorm
     (optimized_v3.py:120-148).  Idempotent for one configuration; raises on a
@@ -294,8 +332,12 @@ def _cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler,
                           loss_backend):
     with amp_context(ids.device, precision):
         hidden = hidden_states(model, ids)
-    leaf = hidden.detach().reshape(-1, hidden.shape[-1]).requires_grad_(True)
     weight = model.lm_head.weight
+    if (loss_backend in ("triton", "hip") and precision == "fp16" and ids.device.type == "cuda"
+            and weight.dtype == torch.float32):
+        return _fused_head(hidden, weight, labels, denominator, chunk_tokens, scaler, precision,
+                           ids.device)
+    leaf = hidden.detach().reshape(-1, hidden.shape[-1]).requires_grad_(True)
     if ids.device.type != "cuda" or precision == "fp32":
         dtype = weight.dtype
     else:

@@ -100,3 +100,30 @@ def test_rejects_cpu_and_bad_inputs(cuda_device):
         TiledCrossEntropy.apply(x, torch.tensor([0, 1, 2], device=cuda_device, dtype=torch.int32))
     with pytest.raises(ValueError, match="Contiguous"):
         TiledCrossEntropy.apply(x.t(), torch.tensor([0, 1, 2], device=cuda_device))
+
+
+@pytest.mark.parametrize("rows,d,vocab", [(1000, 256, 50257), (333, 128, 1001), (64, 256, 64)])
+def test_tied_head_ce_matches_autograd(cuda_device, rows, d, vocab):
+    """The padded-stride head + fused CE (forward and backward in one call)
+    against autograd of autocast F.linear + cross_entropy_sum on the same fp16
+    operands: the same loss and gradients up to the GEMMs' fp32 accumulation
+    order (the padded logits run other hipBLASLt kernels)."""
+    from reversability_amd.kernels import padded_head, tied_head_ce
+    g = torch.Generator().manual_seed(5)
+    x16 = torch.randn(rows, d, generator=g).half().to(cuda_device)
+    w = (0.05 * torch.randn(vocab, d, generator=g)).to(cuda_device)
+    labels = torch.randint(0, vocab, (rows,), generator=g).to(cuda_device)
+    labels[::7] = -100
+    grad = torch.tensor([0.37], device=cuda_device)
+    head16 = padded_head(w)
+    assert head16.shape[0] % 64 == 0 and torch.equal(head16[vocab:], torch.zeros_like(head16[vocab:]))
+    loss, dx16, dw16 = tied_head_ce(x16, head16, vocab, labels, grad)
+    xr = x16.clone().requires_grad_(True)
+    hr = w.half().requires_grad_(True)
+    ref = cross_entropy_sum(torch.nn.functional.linear(xr, hr), labels)
+    (ref * 0.37).backward()
+    assert abs(float(loss) - float(ref)) <= 1e-3 * abs(float(ref))
+    for got, want in ((dx16, xr.grad), (dw16, hr.grad)):
+        assert got.dtype == torch.float16
+        rel = float((got.float() - want.float()).norm() / want.float().norm())
+        assert rel < 2e-3, rel
