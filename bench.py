@@ -246,7 +246,8 @@ def make_train_step(dev, name: str):
     """One full training update of a TRAIN_CONFIGS entry, on the reference's
     v3 probe path (scripts/benchmark_midpoint_v3.py:78-83 over
     scripts/benchmark_optimized.py:54-82): install_v3 (split core for the
-    midpoint config, 8192-token tiled MLP, fused SwiGLU and RMSNorm), the
+    midpoint config, 8192-token tiled MLP keeping its tiles for its backward,
+    fused SwiGLU and RMSNorm), the
     attention projections and the causal attention itself on the MFMA kernels
     (enable_linear, enable_attention), the fused token +
     position embedding adding its token gradient into the tied weight's
@@ -274,7 +275,8 @@ def make_train_step(dev, name: str):
     torch.manual_seed(1337)
     model = build_model({"model": cfg["model"], "method": cfg["method"],
                          "step_size": cfg["step_size"]}).to(dev)
-    install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
     enable_linear(model)
     enable_attention(model)
     enable_embedding(model, into_grad=True)

@@ -99,10 +99,11 @@ class TiledMLP(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, up, down, tokens, fused):
+    def forward(ctx, x, up, down, tokens, fused, keep_tiles=False):
         if tokens < 1:
             raise ValueError("Positive MLP tile size required")
         ctx.tokens, ctx.fused = tokens, fused
+        ctx.tiles = None
         ctx.device = x.device.type
         ctx.amp = torch.is_autocast_enabled(ctx.device)
         ctx.dtype = torch.get_autocast_dtype(ctx.device)
@@ -115,9 +116,13 @@ class TiledMLP(torch.autograd.Function):
             # would produce on every tile
             x16 = mlp.cast_f16(flat.contiguous())
             up16, down16 = mlp.cast_weight(up), mlp.cast_weight(down)
+            tiles = [] if keep_tiles else None
             for start in range(0, flat.shape[0], tokens):
-                o, _ = mlp.up_swiglu(x16[start:start + tokens], up16)
+                o, u = mlp.up_swiglu(x16[start:start + tokens], up16, keep_u=keep_tiles)
                 mlp.down(o, down16, output[start:start + tokens])
+                if keep_tiles:
+                    tiles.append((o, u))
+            ctx.tiles = tiles
             del x16, up16, down16
             ctx.save_for_backward(x, up, down)
             return output.reshape(*x.shape[:-1], down.shape[0])
@@ -144,15 +149,20 @@ class TiledMLP(torch.autograd.Function):
             x16, dy = mlp.cast_f16(flat.contiguous()), dy.contiguous()
             up16, down16 = mlp.cast_weight(up), mlp.cast_weight(down)
             dup, ddown = torch.empty_like(up), torch.empty_like(down)
+            tiles, ctx.tiles = ctx.tiles, None
             for i, start in enumerate(range(0, flat.shape[0], ctx.tokens)):
                 stop = start + ctx.tokens
                 x_t, g = x16[start:stop], dy[start:stop]
-                o, u = mlp.up_swiglu(x_t, up16, keep_u=True)
+                if tiles is not None:  # kept by the forward: the same values
+                    o, u = tiles[i]
+                    tiles[i] = None
+                else:
+                    o, u = mlp.up_swiglu(x_t, up16, keep_u=True)
                 du = mlp.dgate(g, down16, u)
                 mlp.dx(du, up16, dx[start:stop])
                 mlp.wgrad(g, o, du, x_t, ddown, dup, accumulate=i > 0)
                 del o, u, du
-            return dx.reshape_as(x), dup, ddown, None, None
+            return dx.reshape_as(x), dup, ddown, None, None, None
         dup = ddown = None
         with torch.autocast(ctx.device, enabled=False):
             up_c, down_c = up.to(cdt), down.to(cdt)
@@ -172,7 +182,7 @@ class TiledMLP(torch.autograd.Function):
                 del x_c, u, o, g, d_o, du, tile_ddown, tile_dup
         if dup is None:  # no rows
             dup, ddown = torch.zeros_like(up), torch.zeros_like(down)
-        return dx.reshape_as(x), dup, ddown, None, None
+        return dx.reshape_as(x), dup, ddown, None, None, None
 
 
 class SplitMidpoint(torch.autograd.Function):
@@ -276,11 +286,19 @@ def _fused_head(hidden, weight, labels, denominator, chunk_tokens, scaler, preci
     return total
 
 
-def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsnorm=False):
+def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsnorm=False,
+               keep_mlp_tiles=False):
     """Wire the optimized core, tiled MLP, fused SwiGLU and fused RMSNorm
     (optimized_v3.py:120-148).  Idempotent for one configuration; raises on a
-    conflicting reinstall, a non-midpoint optimized core, or a biased MLP."""
-    signature = (core_mode, mlp_tokens, swiglu, rmsnorm)
+    conflicting reinstall, a non-midpoint optimized core, or a biased MLP.
+
+    ``keep_mlp_tiles`` (not in the reference): a TiledMLP forward that runs with
+    gradients enabled keeps its tiles' SwiGLU input and output for its backward
+    instead of recomputing them there.  In the reconstruction backward that is
+    one layer's tiles at a time (C5: 0.8 GB), and one up-projection GEMM per
+    layer and step less; the kept values are the ones the recompute would
+    produce, bit for bit."""
+    signature = (core_mode, mlp_tokens, swiglu, rmsnorm, keep_mlp_tiles)
     if hasattr(model, "_v3_signature"):
         if model._v3_signature != signature:
             raise ValueError("Cannot replace an installed v3 configuration")
@@ -300,7 +318,8 @@ def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsn
                 raise ValueError("Tiled MLP experiment supports frozen bias=False only")
 
             def forward(self, x):
-                return TiledMLP.apply(x, self.up.weight, self.down.weight, mlp_tokens, swiglu)
+                return TiledMLP.apply(x, self.up.weight, self.down.weight, mlp_tokens, swiglu,
+                                      keep_mlp_tiles and torch.is_grad_enabled())
             block.mlp.forward = types.MethodType(forward, block.mlp)
     elif swiglu:
         from .kernels import enable_swiglu

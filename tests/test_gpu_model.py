@@ -264,7 +264,8 @@ def test_bench_path_step_matches_autograd(cuda_device):
     reference = build_model(C4).to(cuda_device)
     candidate = copy.deepcopy(reference)
     reference.backward_mode = "autograd"
-    install_v3(candidate, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True)
+    install_v3(candidate, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
     enable_linear(candidate)
     enable_attention(candidate)
     enable_embedding(candidate, into_grad=True)
@@ -320,3 +321,22 @@ def test_full_step_matches_cpu_oracle(cuda_device):
     assert abs(loss_c.item() - loss_o.item()) <= 2e-2 * abs(loss_o.item())
     for name, g in grads_o.items():
         assert rel_l2(grads_c[name], g) < 2e-2, name
+
+
+def test_tiled_mlp_kept_tiles_bitwise(cuda_device):
+    """TiledMLP keeping its tiles' SwiGLU input/output for the backward gives
+    the same output and gradients, bit for bit, as recomputing them."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 7000, 256, generator=g).to(cuda_device)
+    up = (0.02 * torch.randn(2048, 256, generator=g)).to(cuda_device)
+    down = (0.02 * torch.randn(256, 1024, generator=g)).to(cuda_device)
+    gy = torch.randn(3, 7000, 256, generator=g).to(cuda_device)
+    res = []
+    for keep in (False, True):
+        xs, us, ds = (t.clone().requires_grad_(True) for t in (x, up, down))
+        with torch.autocast("cuda", dtype=torch.float16):
+            out = TiledMLP.apply(xs, us, ds, 8192, True, keep)
+        out.backward(gy)
+        res.append((out.detach(), xs.grad, us.grad, ds.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
