@@ -11,7 +11,8 @@ Eq. 2.8/2.9 Hamiltonian Euler):
 ``_InverseStack`` keeps only the final pair and parameter references; its
 backward walks the layers in reverse, reconstructs each layer's input under
 no_grad, rebuilds that one layer's graph with the forward's autocast mode and
-takes its VJP.  Parameter gradients are returned through autograd (never
+takes its VJP (for Euler the inversion's evaluation of A(p0) is itself the
+graph's, computed once instead of twice; same values).  Parameter gradients are returned through autograd (never
 written to ``.grad``).  On ROCm tensors the residual updates run as fused HIP
 kernels (``residual.midpoint_step`` / ``residual.euler_step``) with the eager
 expression's rounding points.
@@ -57,6 +58,30 @@ def inverse_pair(block, p, q, method, h):
     return previous_p, euler_step(q, block.attn(block.attn_norm(previous_p)), -1)
 
 
+# The Euler reconstruction evaluates A(p0) on the recovered p0 twice -- to
+# invert the step and again in the recompute for the VJP -- on identical bits.
+# With this set the inversion keeps that evaluation's graph for the VJP.
+REUSE_EULER_ATTENTION = True
+
+
+def _euler_inverse_for_vjp(block, p, q):
+    """Invert one Euler step and rebuild its graph with one evaluation of
+    A(p0): p0 = p - M(q) (no graph), a = A(p0) with its graph, q0 = q - a, then
+    next_q = q0 + a and next_p = p0 + M(next_q) as forward_pair computes them.
+    Returns (next_p, next_q, p0, q0) with p0, q0 the graph's leaves."""
+    with torch.no_grad():
+        p0 = euler_step(p, block.mlp(block.mlp_norm(q)), -1)
+    with torch.enable_grad():
+        p0 = p0.detach().requires_grad_(True)
+        attention = block.attn(block.attn_norm(p0))
+        with torch.no_grad():
+            q0 = euler_step(q, attention.detach(), -1)
+        q0 = q0.detach().requires_grad_(True)
+        next_q = euler_step(q0, attention, +1)
+        next_p = euler_step(p0, block.mlp(block.mlp_norm(next_q)), +1)
+    return next_p, next_q, p0, q0
+
+
 class _InverseStack(torch.autograd.Function):
     """Whole-stack Function; backward reconstructs inputs layer by layer."""
 
@@ -83,12 +108,16 @@ class _InverseStack(torch.autograd.Function):
         with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype,
                             cache_enabled=False):
             for block in reversed(ctx.blocks):
-                with torch.no_grad():
-                    p0, q0 = inverse_pair(block, p, q, ctx.method, ctx.h)
+                if ctx.method == "euler" and REUSE_EULER_ATTENTION:
+                    next_p, next_q, p0, q0 = _euler_inverse_for_vjp(block, p, q)
+                else:
+                    with torch.no_grad():
+                        p0, q0 = inverse_pair(block, p, q, ctx.method, ctx.h)
+                    with torch.enable_grad():
+                        p0 = p0.detach().requires_grad_(True)
+                        q0 = q0.detach().requires_grad_(True)
+                        next_p, next_q = forward_pair(block, p0, q0, ctx.method, ctx.h)
                 with torch.enable_grad():
-                    p0 = p0.detach().requires_grad_(True)
-                    q0 = q0.detach().requires_grad_(True)
-                    next_p, next_q = forward_pair(block, p0, q0, ctx.method, ctx.h)
                     local = torch.autograd.grad((next_p, next_q), (p0, q0, *block.parameters()),
                                                 (dp, dq))
                 dp, dq = local[0], local[1]

@@ -340,3 +340,34 @@ def test_tiled_mlp_kept_tiles_bitwise(cuda_device):
         res.append((out.detach(), xs.grad, us.grad, ds.grad))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+def test_euler_attention_reuse_bitwise(cuda_device):
+    """The Euler reconstruction with the inversion's A(p0) reused for the VJP
+    gives the same loss and gradients, bit for bit, as inverting and then
+    recomputing the step."""
+    from reversability_amd import reversible
+    torch.manual_seed(11)
+    cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
+                     "d_model": 256, "d_ff": 512}, "method": "euler", "step_size": 0.5}
+    model = build_model(cfg).to(cuda_device)
+    install_v3(model, core_mode="reference", mlp_tokens=256, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
+    enable_linear(model)
+    enable_attention(model)
+    ids = torch.randint(0, 512, (2, 256), device=cuda_device)
+    runs = []
+    saved = reversible.REUSE_EULER_ATTENTION
+    try:
+        for reuse in (False, True):
+            reversible.REUSE_EULER_ATTENTION = reuse
+            model.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.float16):
+                loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+            loss.backward()
+            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
+    finally:
+        reversible.REUSE_EULER_ATTENTION = saved
+    assert torch.equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
