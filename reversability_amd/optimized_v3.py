@@ -185,12 +185,21 @@ class TiledMLP(torch.autograd.Function):
         return dx.reshape_as(x), dup, ddown, None, None, None
 
 
+# SplitMidpoint's backward evaluates each layer's attention twice on the same
+# input: under no_grad for the inversion, then again with gradients for its
+# VJP.  With this set the first evaluation is made with gradients and its graph
+# (one layer's attention, held through the MLP VJP) serves the VJP: the same
+# values, one attention evaluation per layer less.
+KEEP_SPLIT_ATTENTION = True
+
+
 class SplitMidpoint(torch.autograd.Function):
-    """MLP VJP first, then attention recompute + VJP (optimized_v3.py:66-117).
+    """MLP VJP first, then the attention VJP (optimized_v3.py:66-117).
 
     A detached attention proxy carries the force's dependence on attention, so
-    the MLP graph can be released before attention is rebuilt.  Attention is
-    recomputed (the disclosed extra-compute trade-off).
+    the MLP graph can be released before the attention VJP.  The reference
+    recomputes attention for that VJP (its disclosed extra-compute trade-off);
+    with KEEP_SPLIT_ATTENTION the inversion's attention graph is kept instead.
     """
 
     @staticmethod
@@ -216,8 +225,13 @@ class SplitMidpoint(torch.autograd.Function):
         # rebuild (torch <= 2.10); casts are deterministic, values unchanged.
         with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype, cache_enabled=False):
             for block in reversed(ctx.blocks):
-                with torch.no_grad():
-                    attention = block.attn(block.attn_norm(p))
+                if KEEP_SPLIT_ATTENTION:  # its graph serves the attention VJP below
+                    with torch.enable_grad():
+                        attn_input = p.detach().requires_grad_(True)
+                        attention = block.attn(block.attn_norm(attn_input))
+                else:
+                    with torch.no_grad():
+                        attention = block.attn(block.attn_norm(p))
                 with torch.enable_grad():
                     previous_q = p.detach().requires_grad_(True)
                     proxy = attention.detach().requires_grad_(True)
@@ -232,10 +246,11 @@ class SplitMidpoint(torch.autograd.Function):
                                                 (dp, dq))
                 next_dp, q_mlp, attention_cotangent = local[:3]
                 mlp_grads = local[3:]
-                del attention, proxy, mlp, next_q, local
+                del proxy, mlp, next_q, local
                 with torch.enable_grad():
-                    attn_input = previous_q.detach().requires_grad_(True)
-                    attention = block.attn(block.attn_norm(attn_input))
+                    if not KEEP_SPLIT_ATTENTION:
+                        attn_input = previous_q.detach().requires_grad_(True)
+                        attention = block.attn(block.attn_norm(attn_input))
                     attention_parameters = (*block.attn_norm.parameters(), *block.attn.parameters())
                     attn_local = torch.autograd.grad(attention, (attn_input, *attention_parameters),
                                                      attention_cotangent)

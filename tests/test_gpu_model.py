@@ -371,3 +371,31 @@ def test_euler_attention_reuse_bitwise(cuda_device):
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)
+
+
+def test_split_midpoint_kept_attention_bitwise(cuda_device):
+    """SplitMidpoint with the inversion's attention graph kept for the attention
+    VJP gives the same loss and gradients, bit for bit, as recomputing it."""
+    from reversability_amd import optimized_v3
+    torch.manual_seed(12)
+    model = build_model(C4).to(cuda_device)
+    install_v3(model, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
+    enable_linear(model)
+    enable_attention(model)
+    x, y = _c4_batch(cuda_device, batch=4)
+    runs = []
+    saved = optimized_v3.KEEP_SPLIT_ATTENTION
+    try:
+        for keep in (False, True):
+            optimized_v3.KEEP_SPLIT_ATTENTION = keep
+            model.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.float16):
+                loss = F.cross_entropy(model(x).flatten(0, 1).float(), y.flatten())
+            loss.backward()
+            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
+    finally:
+        optimized_v3.KEEP_SPLIT_ATTENTION = saved
+    assert torch.equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
