@@ -241,6 +241,12 @@ TRAIN_CONFIGS = {
 # 19.4 ms at 1024).  None = the whole batch.
 HEAD_CHUNK = None
 
+# TiledMLP token tile: the reference probes 8192 (scripts/benchmark_midpoint_v3.py),
+# a memory setting for a 16 GB T4; at configs[3] (16896 tokens) it leaves a
+# 512-token third tile whose GEMMs are pure launch latency.  None = one tile of
+# the whole batch (C5's widest tile intermediates: 0.8 GB).
+MLP_TOKENS = None
+
 
 def make_train_step(dev, name: str):
     """One full training update of a TRAIN_CONFIGS entry, on the reference's
@@ -275,7 +281,8 @@ def make_train_step(dev, name: str):
     torch.manual_seed(1337)
     model = build_model({"model": cfg["model"], "method": cfg["method"],
                          "step_size": cfg["step_size"]}).to(dev)
-    install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=8192, swiglu=True, rmsnorm=True,
+    install_v3(model, core_mode=cfg["core_mode"], mlp_tokens=MLP_TOKENS or batch * length,
+               swiglu=True, rmsnorm=True,
                keep_mlp_tiles=True)
     enable_linear(model)
     enable_attention(model)
@@ -318,7 +325,8 @@ def train_step_bench(dev, steps: int, warmup: int, name: str = "c4"):
             "loss": float(loss.item()) / targets, "steps": steps, "warmup": warmup,
             "config": {"workload": cfg["workload"], "global_batch": cfg["batch"],
                        "seq_len": cfg["model"]["max_sequence_length"],
-                       "core_mode": cfg["core_mode"], "mlp_tokens": 8192,
+                       "core_mode": cfg["core_mode"],
+                       "mlp_tokens": MLP_TOKENS or cfg["batch"] * cfg["model"]["max_sequence_length"],
                        "head": f"cached head, {HEAD_CHUNK or 'whole-batch'} token chunks, "
                                "fused CE",
                        "precision": "fp16-autocast"},

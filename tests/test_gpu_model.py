@@ -264,8 +264,8 @@ def test_bench_path_step_matches_autograd(cuda_device):
     reference = build_model(C4).to(cuda_device)
     candidate = copy.deepcopy(reference)
     reference.backward_mode = "autograd"
-    install_v3(candidate, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True,
-               keep_mlp_tiles=True)
+    install_v3(candidate, core_mode="split", mlp_tokens=33 * 512, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)  # bench.py: one MLP tile of the whole batch
     enable_linear(candidate)
     enable_attention(candidate)
     enable_embedding(candidate, into_grad=True)
