@@ -160,6 +160,12 @@ __device__ __forceinline__ float grad_of(float xv, int64_t col, int64_t t, float
   return (col == t ? neg : 0.f) - __expf(logp) * neg;
 }
 
+// Non-target column: grad_of's value with the label test dropped.
+template <typename T>
+__device__ __forceinline__ float grad_off(float xv, float m, float lse, float neg) {
+  return 0.f - __expf(rv::round_to<T>((xv - m) - lse)) * neg;
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads)
 void ce_bwd_k(const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ labels,
@@ -171,26 +177,37 @@ void ce_bwd_k(const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ l
   T* dr = dx + row * ld;
   const RowSplit<T> sp(xr, cols);
   const int64_t t = labels[row];
-  const bool zero = t == ignore;
-  const bool bad = !zero && (t < 0 || t >= cols);
+  const rv::u32x4* xv = reinterpret_cast<const rv::u32x4*>(xr + sp.head);
+  rv::u32x4* dv = reinterpret_cast<rv::u32x4*>(dr + sp.head);
+  if (t == ignore) {  // an ignored row has a zero gradient
+    for (int64_t c = threadIdx.x; c < sp.head; c += kThreads) dr[c] = rv::Conv<T>::from_f(0.f);
+    for (int64_t v = threadIdx.x; v < sp.nvec; v += kThreads)
+      __builtin_nontemporal_store(rv::u32x4{0u, 0u, 0u, 0u}, dv + v);
+    for (int64_t c = sp.tail0 + threadIdx.x; c < cols; c += kThreads)
+      dr[c] = rv::Conv<T>::from_f(0.f);
+    return;
+  }
+  const bool bad = t < 0 || t >= cols;
   const float m = rmax[row], lse = rlse[row];
   const float neg = bad ? NAN : rv::round_to<T>(-grad[0]);
   for (int64_t c = threadIdx.x; c < sp.head; c += kThreads)
-    dr[c] = rv::Conv<T>::from_f(zero ? 0.f : grad_of<T>(load1(xr + c), c, t, m, lse, neg));
-  const rv::u32x4* xv = reinterpret_cast<const rv::u32x4*>(xr + sp.head);
-  rv::u32x4* dv = reinterpret_cast<rv::u32x4*>(dr + sp.head);
+    dr[c] = rv::Conv<T>::from_f(grad_of<T>(load1(xr + c), c, t, m, lse, neg));
 #pragma unroll 4
   for (int64_t v = threadIdx.x; v < sp.nvec; v += kThreads) {
     const rv::u32x4 w = __builtin_nontemporal_load(xv + v);
     rv::u32x4 o;
-    const int64_t c0 = sp.head + v * V;
 #pragma unroll
-    for (int i = 0; i < V; ++i)
-      Elem<T>::set(o, i, zero ? 0.f : grad_of<T>(Elem<T>::get(w, i), c0 + i, t, m, lse, neg));
+    for (int i = 0; i < V; ++i) Elem<T>::set(o, i, grad_off<T>(Elem<T>::get(w, i), m, lse, neg));
+    const int64_t c0 = sp.head + v * V;
+    if (static_cast<uint64_t>(t - c0) < static_cast<uint64_t>(V)) {  // the target's vector
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        if (c0 + i == t) Elem<T>::set(o, i, grad_of<T>(Elem<T>::get(w, i), c0 + i, t, m, lse, neg));
+    }
     __builtin_nontemporal_store(o, dv + v);
   }
   for (int64_t c = sp.tail0 + threadIdx.x; c < cols; c += kThreads)
-    dr[c] = rv::Conv<T>::from_f(zero ? 0.f : grad_of<T>(load1(xr + c), c, t, m, lse, neg));
+    dr[c] = rv::Conv<T>::from_f(grad_of<T>(load1(xr + c), c, t, m, lse, neg));
 }
 
 }  // namespace
