@@ -50,6 +50,11 @@
 // With lanes 4e..4e+3 addressing 16 consecutive halves of LDS row e, lane i
 // receives column i of rows 0..3: a 4 (k) x 16 (row) block, transposed.
 
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "rv_device.h"
 
 namespace {
@@ -623,16 +628,90 @@ int pick_act(int64_t m, int64_t n_cols, bool swiglu) {
   return best;
 }
 
+// Measured tile choice.  The fastest tile shape of an activation GEMM depends
+// on more than the grid size (how the last round of workgroups fills the
+// chip, two workgroups per CU overlapping one's epilogue with the other's
+// MFMAs, the k loop's length), and the shape never changes a result bit: every
+// output element sums its k blocks in the same order in every shape.  So the
+// first call for each (epilogue, operand layouts, m, n, k) times every shape
+// that fits (one warm-up launch, then two timed ones on the caller's stream,
+// which is synchronised once) and keeps the fastest.  The epilogues tuned
+// here overwrite their outputs, so the extra launches write the same values.
+// Calls made while the stream is being captured, or with RV_GEMM_TUNE=0 in
+// the environment, use pick_act's rule.
+using TuneKey = std::tuple<int, int, int, int64_t, int64_t, int64_t>;
+std::mutex g_tune_mu;
+std::map<TuneKey, int> g_tuned;
+
+bool tuning_enabled(hipStream_t s) {
+  static const bool on = [] {
+    const char* v = std::getenv("RV_GEMM_TUNE");
+    return !(v && v[0] == '0');
+  }();
+  if (!on) return false;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+  return st == hipStreamCaptureStatusNone;
+}
+
 template <bool A_RC, bool B_RC, Epi EPI>
-int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
+int launch_shape(int shape, GemmArgs a, int64_t n_cols, hipStream_t s) {
   const bool swiglu = EPI == Epi::SwiGLU;
-  const int shape = pick_act(a.m, n_cols, swiglu);
-  if (shape < 0) return RV_ERR_UNSUPPORTED;
   const TileShape t = kShapes[shape];
   a.tiles_m = (a.m + t.bm - 1) / t.bm;
   a.tiles_n = n_cols / (swiglu ? t.bn / 2 : t.bn);
   a.k_chunk = a.k;
   return launch<A_RC, B_RC, EPI>(shape, a, 1, s);
+}
+
+template <bool A_RC, bool B_RC, Epi EPI>
+int tune_act(const GemmArgs& a, int64_t n_cols, hipStream_t s, int fallback) {
+  const bool swiglu = EPI == Epi::SwiGLU;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return fallback;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return fallback;
+  }
+  int best = fallback;
+  float best_ms = 0.f;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t cols = swiglu ? kShapes[i].bn / 2 : kShapes[i].bn;
+    if (n_cols % cols) continue;
+    if (launch_shape<A_RC, B_RC, EPI>(i, a, n_cols, s) != RV_OK) continue;
+    bool ok = hipEventRecord(e0, s) == hipSuccess;
+    ok = ok && launch_shape<A_RC, B_RC, EPI>(i, a, n_cols, s) == RV_OK;
+    ok = ok && launch_shape<A_RC, B_RC, EPI>(i, a, n_cols, s) == RV_OK;
+    ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+    float ms = 0.f;
+    ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    if (ok && (best_ms == 0.f || ms < best_ms)) best = i, best_ms = ms;
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return best;
+}
+
+template <bool A_RC, bool B_RC, Epi EPI>
+int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
+  const bool swiglu = EPI == Epi::SwiGLU;
+  int shape = pick_act(a.m, n_cols, swiglu);
+  if (shape < 0) return RV_ERR_UNSUPPORTED;
+  if (tuning_enabled(s)) {
+    int device = 0;
+    (void)hipGetDevice(&device);
+    const TuneKey key{(int)EPI * 4 + (A_RC ? 2 : 0) + (B_RC ? 1 : 0), device, 0, a.m, n_cols,
+                      a.k};
+    std::lock_guard<std::mutex> lock(g_tune_mu);
+    const auto it = g_tuned.find(key);
+    if (it != g_tuned.end()) {
+      shape = it->second;
+    } else {
+      shape = tune_act<A_RC, B_RC, EPI>(a, n_cols, s, shape);
+      g_tuned[key] = shape;
+    }
+  }
+  return launch_shape<A_RC, B_RC, EPI>(shape, a, n_cols, s);
 }
 
 // Weight-gradient plan for an ni x nj output reduced over `rows` tokens: tile
