@@ -297,6 +297,18 @@ int rv_ce_bwd(const void* logits, int dtype, int64_t ld, const int64_t* labels,
               int64_t rows, int64_t cols, int64_t ignore_index, void* dlogits,
               void* stream);
 
+/* rv_ce_fwd followed by rv_ce_bwd in one pass over the logits (each row is
+ * read once and kept in registers), with the same results bit for bit; for
+ * callers that know the upstream gradient *grad before the forward (the tied
+ * head's chunked trainer, src/reversibility/optimized_v3.py:168-186, which
+ * runs the loss forward and backward of one chunk back to back).  fp16 only and
+ * cols <= 65536 (else RV_ERR_UNSUPPORTED: use the two calls).  dlogits may
+ * be logits itself (in place). */
+int rv_ce_fused(const void* logits, int dtype, int64_t ld, const int64_t* labels,
+                int64_t rows, int64_t cols, int64_t ignore_index, const float* grad,
+                float* row_max, float* row_lse, float* loss, void* dlogits,
+                void* stream);
+
 /* ------------------------------------------------------------------------
  * Causal self-attention (F.scaled_dot_product_attention(q, k, v,
  * is_causal=True), default scale 1/sqrt(head_dim), src/reversibility/

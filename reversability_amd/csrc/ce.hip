@@ -210,6 +210,113 @@ void ce_bwd_k(const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ l
     dr[c] = rv::Conv<T>::from_f(grad_of<T>(load1(xr + c), c, t, m, lse, neg));
 }
 
+// Forward and backward of one row in one pass over HBM: the row's 16-byte
+// vectors stay in registers (NV per thread, the same thread-to-vector
+// assignment and reduction order as ce_fwd_k), so the statistics, the loss and
+// the gradient are those of ce_fwd_k followed by ce_bwd_k, bit for bit, with
+// the row read once.  Needs the upstream gradient before the pass (the tied
+// head's trainer knows it: scale / denominator).
+template <typename T, int NV>
+__global__ __launch_bounds__(kThreads)
+void ce_fused_k(const T* __restrict__ x, int64_t ld, const int64_t* __restrict__ labels,
+                int64_t cols, int64_t ignore, const float* __restrict__ grad,
+                float* __restrict__ rmax, float* __restrict__ rlse, float* __restrict__ loss,
+                T* __restrict__ dx) {
+  constexpr int V = Elem<T>::kPerVec;
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ld;
+  T* dr = dx + row * ld;
+  const RowSplit<T> sp(xr, cols);
+  const rv::u32x4* xv = reinterpret_cast<const rv::u32x4*>(xr + sp.head);
+  rv::u32x4* dv = reinterpret_cast<rv::u32x4*>(dr + sp.head);
+  rv::u32x4 r[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t v = threadIdx.x + (int64_t)i * kThreads;
+    r[i] = v < sp.nvec ? __builtin_nontemporal_load(xv + v) : rv::u32x4{0u, 0u, 0u, 0u};
+  }
+  float m = -INFINITY, s = 0.f;
+  for (int64_t c = threadIdx.x; c < sp.head; c += kThreads) add(m, s, load1(xr + c));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    if (threadIdx.x + (int64_t)i * kThreads >= sp.nvec) break;
+    float e[V];
+    float vm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      e[k] = Elem<T>::get(r[i], k);
+      vm = fmaxf(vm, e[k]);
+    }
+    const float n = fmaxf(m, vm);
+    float acc = m == -INFINITY ? 0.f : s * __expf(m - n);
+#pragma unroll
+    for (int k = 0; k < V; ++k) acc = acc + __expf(e[k] - n);
+    m = n;
+    s = acc;
+  }
+  for (int64_t c = sp.tail0 + threadIdx.x; c < cols; c += kThreads) add(m, s, load1(xr + c));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64);
+    const float s2 = __shfl_xor(s, off, 64);
+    merge(m, s, m2, s2);
+  }
+  __shared__ float wm[kWaves], ws[kWaves], stat[2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    wm[wave] = m;
+    ws[wave] = s;
+  }
+  __syncthreads();
+  const int64_t t = labels[row];
+  if (threadIdx.x == 0) {
+    float M = wm[0], S = ws[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) merge(M, S, wm[w], ws[w]);
+    const float lse = logf(S);
+    rmax[row] = M;
+    rlse[row] = lse;
+    float l;
+    if (t == ignore) l = 0.f;
+    else if (t < 0 || t >= cols) l = NAN;
+    else l = -rv::round_to<T>((load1(xr + t) - M) - lse);
+    loss[row] = l;
+    stat[0] = M;
+    stat[1] = lse;
+  }
+  __syncthreads();
+  if (t == ignore) {
+    for (int64_t c = threadIdx.x; c < sp.head; c += kThreads) dr[c] = rv::Conv<T>::from_f(0.f);
+    for (int64_t v = threadIdx.x; v < sp.nvec; v += kThreads)
+      __builtin_nontemporal_store(rv::u32x4{0u, 0u, 0u, 0u}, dv + v);
+    for (int64_t c = sp.tail0 + threadIdx.x; c < cols; c += kThreads)
+      dr[c] = rv::Conv<T>::from_f(0.f);
+    return;
+  }
+  const float M = stat[0], lse = stat[1];
+  const bool bad = t < 0 || t >= cols;
+  const float neg = bad ? NAN : rv::round_to<T>(-grad[0]);
+  for (int64_t c = threadIdx.x; c < sp.head; c += kThreads)
+    dr[c] = rv::Conv<T>::from_f(grad_of<T>(load1(xr + c), c, t, M, lse, neg));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t v = threadIdx.x + (int64_t)i * kThreads;
+    if (v >= sp.nvec) break;
+    rv::u32x4 o;
+#pragma unroll
+    for (int k = 0; k < V; ++k) Elem<T>::set(o, k, grad_off<T>(Elem<T>::get(r[i], k), M, lse, neg));
+    const int64_t c0 = sp.head + v * V;
+    if (static_cast<uint64_t>(t - c0) < static_cast<uint64_t>(V)) {
+#pragma unroll
+      for (int k = 0; k < V; ++k)
+        if (c0 + k == t) Elem<T>::set(o, k, grad_of<T>(Elem<T>::get(r[i], k), c0 + k, t, M, lse, neg));
+    }
+    __builtin_nontemporal_store(o, dv + v);
+  }
+  for (int64_t c = sp.tail0 + threadIdx.x; c < cols; c += kThreads)
+    dr[c] = rv::Conv<T>::from_f(grad_of<T>(load1(xr + c), c, t, M, lse, neg));
+}
+
 }  // namespace
 
 extern "C" {
@@ -256,6 +363,46 @@ int rv_ce_bwd(const void* logits, int dtype, int64_t ld, const int64_t* labels,
                        static_cast<float*>(dlogits));
   else
     return RV_ERR_UNSUPPORTED;
+  return rv_host::check_launch();
+}
+
+int rv_ce_fused(const void* logits, int dtype, int64_t ld, const int64_t* labels, int64_t rows,
+                int64_t cols, int64_t ignore_index, const float* grad, float* row_max,
+                float* row_lse, float* loss, void* dlogits, void* stream) {
+  if (!logits || !labels || !grad || !row_max || !row_lse || !loss || !dlogits)
+    return RV_ERR_NULL_POINTER;
+  if (rows < 0 || cols <= 0 || ld < cols) return RV_ERR_BAD_SIZE;
+  if (rows == 0) return RV_OK;
+  if (rows > 0x7fffffff || dtype != RV_F16) return RV_ERR_UNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(logits) & 15) != (reinterpret_cast<uintptr_t>(dlogits) & 15))
+    return RV_ERR_UNSUPPORTED;
+  // vectors per thread the row needs (upper bound: the scalar head takes < 8)
+  const int64_t per = (cols / 8 + kThreads - 1) / kThreads;
+  const hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)rows), block(kThreads);
+  const __half* x = static_cast<const __half*>(logits);
+  __half* d = static_cast<__half*>(dlogits);
+#define RV_CE_FUSED(NV)                                                                      \
+  case NV:                                                                                   \
+    hipLaunchKernelGGL((ce_fused_k<__half, NV>), grid, block, 0, s, x, ld, labels, cols,      \
+                       ignore_index, grad, row_max, row_lse, loss, d);                       \
+    break
+  // registers per thread: the row's vectors (one instantiation per count, so a
+  // row holds no more registers than it needs and occupancy stays as high as
+  // it can: 50257 columns take 25 vectors per thread)
+  switch (per < 1 ? 1 : per) {
+    RV_CE_FUSED(1); RV_CE_FUSED(2); RV_CE_FUSED(3); RV_CE_FUSED(4);
+    RV_CE_FUSED(5); RV_CE_FUSED(6); RV_CE_FUSED(7); RV_CE_FUSED(8);
+    RV_CE_FUSED(9); RV_CE_FUSED(10); RV_CE_FUSED(11); RV_CE_FUSED(12);
+    RV_CE_FUSED(13); RV_CE_FUSED(14); RV_CE_FUSED(15); RV_CE_FUSED(16);
+    RV_CE_FUSED(17); RV_CE_FUSED(18); RV_CE_FUSED(19); RV_CE_FUSED(20);
+    RV_CE_FUSED(21); RV_CE_FUSED(22); RV_CE_FUSED(23); RV_CE_FUSED(24);
+    RV_CE_FUSED(25); RV_CE_FUSED(26); RV_CE_FUSED(27); RV_CE_FUSED(28);
+    RV_CE_FUSED(29); RV_CE_FUSED(30); RV_CE_FUSED(31); RV_CE_FUSED(32);
+    default:
+      return RV_ERR_UNSUPPORTED;  // rows wider than 65536 take the two-pass kernels
+  }
+#undef RV_CE_FUSED
   return rv_host::check_launch();
 }
 

@@ -61,6 +61,8 @@ def cross_entropy_sum(logits, labels):
 
 
 VOCAB_ALIGN = 64  # padded logits row stride (in elements) of tied_head_ce
+# widest row rv_ce_fused keeps in registers (32 16-byte vectors per thread)
+FUSED_CE_MAX_COLS = 65536
 
 
 def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: torch.Tensor,
@@ -71,7 +73,8 @@ def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: to
     The same computation as ``cross_entropy_sum(F.linear(x16, head16[:vocab]),
     labels)`` under fp16 autocast followed by its backward with upstream
     gradient ``grad`` (a device fp32 scalar): logits = fp16(x16 W^T); loss and
-    dlogits from the fused cross-entropy kernels; dx = dlogits W and
+    dlogits from one pass of rv_ce_fused over each logits row (the two-pass
+    rv_ce_fwd / rv_ce_bwd above FUSED_CE_MAX_COLS, same bits); dx = dlogits W and
     dW = dlogits^T x16 (fp16, as autocast's linear produces them).  ``head16`` is
     the fp16 head with its rows padded to a multiple of VOCAB_ALIGN (the pad
     rows zero), so every logits row starts 16-byte aligned: with the odd
@@ -92,15 +95,22 @@ def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: to
     logits = torch.mm(x16, head16.t())                       # [rows, padded] fp16
     rmax, rlse, losses = (torch.empty(rows, device=x16.device, dtype=torch.float32)
                           for _ in range(3))
-    dlogits = torch.empty_like(logits)
     st = _stream(x16)
-    if rows:
-        _check(lib.rv_ce_fwd(logits.data_ptr(), RV_F16, padded, labels.data_ptr(), rows, vocab,
-                             IGNORE_INDEX, rmax.data_ptr(), rlse.data_ptr(), losses.data_ptr(),
-                             st), "rv_ce_fwd")
-        _check(lib.rv_ce_bwd(logits.data_ptr(), RV_F16, padded, labels.data_ptr(),
-                             rmax.data_ptr(), rlse.data_ptr(), grad.data_ptr(), rows, vocab,
-                             IGNORE_INDEX, dlogits.data_ptr(), st), "rv_ce_bwd")
+    if rows and vocab <= FUSED_CE_MAX_COLS:
+        # one pass: loss and gradient, written over the logits
+        dlogits = logits
+        _check(lib.rv_ce_fused(logits.data_ptr(), RV_F16, padded, labels.data_ptr(), rows, vocab,
+                               IGNORE_INDEX, grad.data_ptr(), rmax.data_ptr(), rlse.data_ptr(),
+                               losses.data_ptr(), dlogits.data_ptr(), st), "rv_ce_fused")
+    else:
+        dlogits = torch.empty_like(logits)
+        if rows:
+            _check(lib.rv_ce_fwd(logits.data_ptr(), RV_F16, padded, labels.data_ptr(), rows,
+                                 vocab, IGNORE_INDEX, rmax.data_ptr(), rlse.data_ptr(),
+                                 losses.data_ptr(), st), "rv_ce_fwd")
+            _check(lib.rv_ce_bwd(logits.data_ptr(), RV_F16, padded, labels.data_ptr(),
+                                 rmax.data_ptr(), rlse.data_ptr(), grad.data_ptr(), rows, vocab,
+                                 IGNORE_INDEX, dlogits.data_ptr(), st), "rv_ce_bwd")
     del logits
     d_view = dlogits[:, :vocab]
     dx16 = torch.mm(d_view, head16[:vocab])

@@ -113,3 +113,19 @@ def test_rmsnorm_fp16_entry_points_validate_without_device():
     assert lib.rv_rmsnorm_fwd_f16(fake, fake, ctypes.c_void_p(4098), fake, 4, 256, 1e-7,
                                   None) == 3  # fp16 output must be 8-byte aligned
     assert lib.rv_rmsnorm_bwd_f16(fake, fake, fake, fake, fake, fake, None, 0, 4, 256, None) == 4
+
+
+def test_fused_cross_entropy_validates_without_device():
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)
+    args = lambda x, dt, ld, rows, cols, d: (x, dt, ld, fake, rows, cols, -100, fake, fake, fake,
+                                             fake, d, None)
+    assert lib.rv_ce_fused(*args(None, _hip.RV_F16, 8, 4, 8, fake)) == 1
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 8, 4, 8, None)) == 1
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 7, 4, 8, fake)) == 2   # ld < cols
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 8, -1, 8, fake)) == 2
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 8, 0, 8, fake)) == 0   # nothing to do
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F32, 8, 4, 8, fake)) == 3   # fp16 only
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 65544, 4, 65544, fake)) == 3  # too wide
+    # logits and dlogits must share their address modulo 16
+    assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 8, 4, 8, ctypes.c_void_p(4098))) == 3

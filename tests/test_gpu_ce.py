@@ -127,3 +127,113 @@ def test_tied_head_ce_matches_autograd(cuda_device, rows, d, vocab):
         assert got.dtype == torch.float16
         rel = float((got.float() - want.float()).norm() / want.float().norm())
         assert rel < 2e-3, rel
+
+
+def _fused_vs_two_pass(lib, flat, offset, ld, cols, y, grad, in_place):
+    """rv_ce_fused on the rows of stride ld starting at flat[offset] (first cols
+    used) against rv_ce_fwd followed by rv_ce_bwd on a copy; returns both
+    (row max, lse, loss, dlogits).  Copies keep flat's address modulo 16."""
+    from reversability_amd._hip import RV_F16, _stream
+    rows = y.numel()
+    dev = flat.device
+    outs = []
+    for fused in (True, False):
+        xs = flat.clone()
+        x = xs[offset:offset + rows * ld]
+        st = [torch.full((rows,), 7.0, device=dev) for _ in range(3)]
+        d = x if (fused and in_place) else torch.full_like(xs, 3.0)[offset:offset + rows * ld]
+        assert (x.data_ptr() - d.data_ptr()) % 16 == 0
+        ptrs = [t.data_ptr() for t in st]
+        if fused:
+            rc = lib.rv_ce_fused(x.data_ptr(), RV_F16, ld, y.data_ptr(), rows, cols, -100,
+                                 grad.data_ptr(), *ptrs, d.data_ptr(), _stream(xs))
+            assert rc == 0
+        else:
+            assert lib.rv_ce_fwd(x.data_ptr(), RV_F16, ld, y.data_ptr(), rows, cols, -100,
+                                 *ptrs, _stream(xs)) == 0
+            assert lib.rv_ce_bwd(x.data_ptr(), RV_F16, ld, y.data_ptr(), ptrs[0], ptrs[1],
+                                 grad.data_ptr(), rows, cols, -100, d.data_ptr(),
+                                 _stream(xs)) == 0
+        torch.cuda.synchronize()
+        outs.append((*st, d.view(rows, ld)))
+    return outs
+
+
+def _same_bits(a, b):
+    return torch.equal(a.view(torch.int16) if a.dtype == torch.float16 else a.view(torch.int32),
+                       b.view(torch.int16) if b.dtype == torch.float16 else b.view(torch.int32))
+
+
+@pytest.mark.parametrize("rows,cols,ld,offset", [
+    (64, 50257, 50304, 0),     # the tied head's padded stride
+    (37, 50257, 50257, 0),     # odd stride: every row has a scalar head and tail
+    (19, 65536, 65536, 0),     # widest row the registers hold
+    (11, 65535, 65536, 3),     # misaligned base, 32 vectors per thread
+    (23, 2048, 2051, 5),
+    (9, 7, 8, 1),              # no vector part
+    (5, 1, 1, 0),
+    (256, 3000, 3072, 0),
+])
+@pytest.mark.parametrize("in_place", [False, True])
+def test_fused_matches_two_pass_bitwise(cuda_device, rows, cols, ld, offset, in_place):
+    """rv_ce_fused = rv_ce_fwd then rv_ce_bwd, bit for bit (row max, lse,
+    loss, every written dlogits element incl. ignored and bad-label rows);
+    the padding past cols is left as it was."""
+    from reversability_amd._hip import library
+    g = torch.Generator().manual_seed(rows + cols)
+    flat = (4 * torch.randn(rows * ld + offset, generator=g)).half().to(cuda_device)
+    y = torch.randint(0, cols, (rows,), generator=g)
+    y[::4] = -100
+    if rows > 5:
+        y[1], y[2], y[3] = cols - 1, cols, -7   # last column; two bad labels
+    y = y.to(cuda_device)
+    if rows > 5 and cols > 64:
+        # a row spanning the fp16 range: exp(logp) underflows (zero-signed gradients)
+        flat[offset + 5 * ld:offset + 5 * ld + cols] = torch.linspace(
+            -60000.0, 8.0, cols, device=cuda_device).half()
+    grad = torch.tensor([0.3125], device=cuda_device)
+    (fm, fl, floss, fd), (tm, tl, tloss, td) = _fused_vs_two_pass(library(), flat, offset, ld, cols,
+                                                                   y, grad, in_place)
+    assert _same_bits(fm, tm) and _same_bits(fl, tl) and _same_bits(floss, tloss)
+    assert _same_bits(fd[:, :cols], td[:, :cols])
+    if ld > cols and not in_place:
+        assert bool((fd[:, cols:] == 3.0).all())
+    if rows > 5:
+        assert torch.isnan(floss[2]) and torch.isnan(floss[3])
+        assert torch.isnan(fd[2, :cols].float()).all()
+    assert torch.count_nonzero(fd[::4, :cols]) == 0
+
+
+def test_fused_matches_oracle_and_rejects_wide_rows(cuda_device):
+    """Against the CPU oracle (loss within one fp16 ulp, dlogits within one ulp
+    given the kernel's own statistics), and RV_ERR_UNSUPPORTED for fp32 and
+    rows wider than 65536 (the caller takes the two-pass kernels)."""
+    from reversability_amd._hip import RV_F16, RV_F32, _stream, library
+    lib = library()
+    rows, cols = 200, 50257
+    g = torch.Generator().manual_seed(9)
+    x = (3 * torch.randn(rows, cols, generator=g)).half()
+    y = torch.randint(0, cols, (rows,), generator=g)
+    y[::5] = -100
+    xd, yd = x.to(cuda_device), y.to(cuda_device)
+    grad = torch.tensor([0.75], device=cuda_device)
+    rmax, rlse, loss = (torch.empty(rows, device=cuda_device) for _ in range(3))
+    dx = torch.empty_like(xd)
+    assert lib.rv_ce_fused(xd.data_ptr(), RV_F16, cols, yd.data_ptr(), rows, cols, -100,
+                           grad.data_ptr(), rmax.data_ptr(), rlse.data_ptr(), loss.data_ptr(),
+                           dx.data_ptr(), _stream(xd)) == 0
+    omax, olse, oloss = oracle.ce_fwd(x.numpy(), y.numpy())
+    assert np.array_equal(rmax.cpu().numpy(), omax)
+    lg = loss.cpu().numpy()
+    assert np.all(np.abs(lg - oloss) <= ulp16(oloss))
+    odx = oracle.ce_bwd(x.numpy(), y.numpy(), rmax.cpu().numpy(), rlse.cpu().numpy(), 0.75)
+    dg, do = dx.cpu().numpy().astype(np.float64), odx.astype(np.float64)
+    assert np.all(np.abs(dg - do) <= ulp16(do) + 1e-12)
+    assert np.mean(dg == do) > 0.99
+    RV_ERR_UNSUPPORTED = 3  # include/reversibility_hip.h
+    wide = torch.zeros(2, 65544, device=cuda_device, dtype=torch.float16)
+    y2 = torch.zeros(2, device=cuda_device, dtype=torch.int64)
+    args = (y2.data_ptr(), 2, 65544, -100, grad.data_ptr(), rmax.data_ptr(), rlse.data_ptr(),
+            loss.data_ptr(), wide.data_ptr(), _stream(wide))
+    assert lib.rv_ce_fused(wide.data_ptr(), RV_F16, 65544, *args) == RV_ERR_UNSUPPORTED
+    assert lib.rv_ce_fused(wide.data_ptr(), RV_F32, 65544, *args) == RV_ERR_UNSUPPORTED
