@@ -68,7 +68,22 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // 16-byte stag
 
 constexpr int kThreads = 256;
 constexpr int kBK = 32;             // k per pipeline stage
-constexpr int kStages = 4;          // depth of the LDS ring
+#ifndef RV_ST_256x256
+#define RV_ST_256x256 4
+#endif
+#ifndef RV_ST_128x256
+#define RV_ST_128x256 3
+#endif
+#ifndef RV_ST_128x128
+#define RV_ST_128x128 4
+#endif
+#ifndef RV_ST_64x128
+#define RV_ST_64x128 4
+#endif
+// depth of the LDS ring per tile shape
+constexpr int stages_for(int bm, int bn) {
+  return bm == 256 ? RV_ST_256x256 : bn == 256 ? RV_ST_128x256 : bm == 128 ? RV_ST_128x128 : RV_ST_64x128;
+}
 constexpr int kCUs = 256;           // MI355X compute units (tile-shape choice only)
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, gfx9 data format
 
@@ -273,6 +288,7 @@ template <int BM, int BN, bool A_RC, bool B_RC, Epi EPI>
 __global__ __launch_bounds__(kThreads)
 void gemm_kernel(GemmArgs args) {
   constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int kStages = stages_for(BM, BN);
   constexpr int kA = BM * kBK, kB = BN * kBK;          // halves per stage and operand
   constexpr int kRing = kStages * (kA + kB);
   constexpr int kStaging = 4 * (BM / 2) * (BN / 2 + 8);  // fp16 epilogue staging
