@@ -306,23 +306,46 @@ def make_train_step(dev, name: str):
         scaler.update()
         return loss
 
+    step.model, step.opt, step.scaler = model, opt, scaler
     return step, targets, cfg
 
 
-def train_step_bench(dev, steps: int, warmup: int, name: str = "c4"):
-    """Tokens/s of one TRAIN_CONFIGS entry's full training update."""
+def train_step_bench(dev, steps: int, warmup: int, name: str = "c4", graph: bool = True):
+    """Tokens/s of one TRAIN_CONFIGS entry's full training update: ``steps``
+    replays of the update captured in a HIP graph (reversability_amd.graph;
+    ``warmup`` eager updates precede the capture), and the same number of
+    eager updates of a second copy for comparison (host-launched, every
+    kernel enqueued from Python)."""
+    import gc
     import torch
+    from reversability_amd.graph import CapturedStep
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps, out
+
     step, targets, cfg = make_train_step(dev, name)
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        loss = step()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
+    dt_eager, loss_eager = timed(step)
+    loss_eager = float(loss_eager.item())
+    dt, loss = dt_eager, loss_eager
+    if graph:
+        del step
+        gc.collect()
+        torch.cuda.empty_cache()
+        step, targets, cfg = make_train_step(dev, name)
+        captured = CapturedStep(step, warmup)
+        dt, out = timed(captured)
+        loss = float(out.item())
     return {"tokens_per_s": targets / dt, "ms_per_step": dt * 1e3,
-            "loss": float(loss.item()) / targets, "steps": steps, "warmup": warmup,
+            "launch": "HIP graph of the whole update, replayed" if graph else "eager",
+            "eager_tokens_per_s": targets / dt_eager, "eager_ms_per_step": dt_eager * 1e3,
+            "loss": loss / targets, "steps": steps, "warmup": warmup,
             "config": {"workload": cfg["workload"], "global_batch": cfg["batch"],
                        "seq_len": cfg["model"]["max_sequence_length"],
                        "core_mode": cfg["core_mode"],

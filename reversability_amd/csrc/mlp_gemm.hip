@@ -653,21 +653,25 @@ int pick_act(int64_t m, int64_t n_cols, bool swiglu) {
 // that fits (one warm-up launch, then two timed ones on the caller's stream,
 // which is synchronised once) and keeps the fastest.  The epilogues tuned
 // here overwrite their outputs, so the extra launches write the same values.
-// Calls made while the stream is being captured, or with RV_GEMM_TUNE=0 in
-// the environment, use pick_act's rule.
+// A call made while its stream is being captured into a graph never tunes
+// (that would synchronise): it takes the shape already chosen for its key,
+// else pick_act's rule.  RV_GEMM_TUNE=0 in the environment turns tuning off.
 using TuneKey = std::tuple<int, int, int, int64_t, int64_t, int64_t>;
 std::mutex g_tune_mu;
 std::map<TuneKey, int> g_tuned;
 
-bool tuning_enabled(hipStream_t s) {
+bool tuning_enabled() {
   static const bool on = [] {
     const char* v = std::getenv("RV_GEMM_TUNE");
     return !(v && v[0] == '0');
   }();
-  if (!on) return false;
+  return on;
+}
+
+bool capturing(hipStream_t s) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
-  return st == hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) return true;  // then do not tune
+  return st != hipStreamCaptureStatusNone;
 }
 
 template <bool A_RC, bool B_RC, Epi EPI>
@@ -713,7 +717,7 @@ int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
   const bool swiglu = EPI == Epi::SwiGLU;
   int shape = pick_act(a.m, n_cols, swiglu);
   if (shape < 0) return RV_ERR_UNSUPPORTED;
-  if (tuning_enabled(s)) {
+  if (tuning_enabled()) {
     int device = 0;
     (void)hipGetDevice(&device);
     const TuneKey key{(int)EPI * 4 + (A_RC ? 2 : 0) + (B_RC ? 1 : 0), device, 0, a.m, n_cols,
@@ -722,7 +726,7 @@ int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
     const auto it = g_tuned.find(key);
     if (it != g_tuned.end()) {
       shape = it->second;
-    } else {
+    } else if (!capturing(s)) {
       shape = tune_act<A_RC, B_RC, EPI>(a, n_cols, s, shape);
       g_tuned[key] = shape;
     }

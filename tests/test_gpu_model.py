@@ -399,3 +399,35 @@ def test_split_midpoint_kept_attention_bitwise(cuda_device):
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)
+
+
+def test_captured_train_step_matches_eager_bitwise(cuda_device):
+    """The whole configs[3] update (bench.make_train_step: batch cut on the
+    device, fp16 core forward and reconstruction backward, tied head and fused
+    cross-entropy, GradScaler unscale, clip, FusedAdamW) captured once in a
+    HIP graph and replayed equals the eager update of a twin model bit for
+    bit -- loss, every parameter, the loss scale -- after each of three
+    replays, with the twin's eager updates and host synchronisations between
+    the replays.  Replays must also change the parameters (the graph is not
+    a no-op)."""
+    import bench
+    from reversability_amd.graph import CapturedStep
+    eager, _, _ = bench.make_train_step(cuda_device, "c4")
+    graphed, _, _ = bench.make_train_step(cuda_device, "c4")
+    captured = CapturedStep(graphed, warmup=3)
+    for _ in range(3):  # the capture's warm-up updates
+        eager()
+    torch.cuda.synchronize()
+    before = [p.detach().clone() for p in graphed.model.parameters()]
+    for i in range(3):
+        print(f"  replay {i}", flush=True)
+        loss_g = captured().clone()
+        torch.cuda.synchronize()
+        loss_e = eager()
+        torch.cuda.synchronize()
+        assert torch.equal(loss_g, loss_e), (i, float(loss_g), float(loss_e))
+        for (name, pe), pg in zip(eager.model.named_parameters(), graphed.model.parameters()):
+            assert torch.equal(pe, pg), (i, name)
+        assert torch.equal(eager.scaler._scale, graphed.scaler._scale)
+    changed = sum(not torch.equal(b, p) for b, p in zip(before, graphed.model.parameters()))
+    assert changed == len(before)
