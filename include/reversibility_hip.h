@@ -249,6 +249,17 @@ int rv_linear_dw(const void* dy, const void* x, int64_t ldx, int64_t rows,
                  int64_t in, int64_t out, float* dw, int accumulate,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Tile-shape control of the activation GEMMs above (rv_mlp_up_swiglu,
+ * rv_mlp_down, rv_mlp_dgate, rv_mlp_dx, rv_linear_fwd, rv_linear_dx).  No
+ * counterpart in the reference (cuBLAS picks its own kernels): a diagnostic
+ * and test hook.  The shape never changes a result bit.  By default each
+ * (epilogue, layouts, m, n, k) takes the fastest shape measured on its first
+ * call; rv_gemm_force_shape(i) makes every later call use shape i
+ * (0 <= i < rv_gemm_num_shapes(); RV_ERR_UNSUPPORTED from a call whose width
+ * the shape does not divide), -1 restores the default.  Process-wide. */
+int rv_gemm_num_shapes(void);
+int rv_gemm_force_shape(int shape);
+
 /* ------------------------------------------------------------------------
  * AdamW (decoupled weight decay) over fp32 parameters, torch.optim.AdamW's
  * arithmetic and operation order, as the training step drives it through

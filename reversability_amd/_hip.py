@@ -60,6 +60,8 @@ SIGNATURES = {
     "rv_adamw_step": (_I, [_I, _P, _P, _P, _P, _P, _D, _D, _D, _D, _D, _P, _P, _P, _P]),
     "rv_ce_fwd": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "rv_ce_bwd": (_I, [_P, _I, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
+    "rv_gemm_num_shapes": (_I, []),
+    "rv_gemm_force_shape": (_I, [_I]),
     "rv_ce_fused": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "rv_mlp_up_swiglu": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "rv_mlp_down": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),

@@ -50,6 +50,7 @@
 // With lanes 4e..4e+3 addressing 16 consecutive halves of LDS row e, lane i
 // receives column i of rows 0..3: a 4 (k) x 16 (row) block, transposed.
 
+#include <atomic>
 #include <cstdlib>
 #include <map>
 #include <mutex>
@@ -122,15 +123,16 @@ struct MapDirect {  // row0 + r, clamped to the last valid row (results never st
   }
 };
 // SwiGLU up projection: a BN-row B tile holds BN/2 output columns, as gate
-// and value halves per wave column: rows [wn*BN/2, wn*BN/2 + BN/4) are gate
-// rows col0 + wn*BN/4 + w, the next BN/4 are the value rows f + the same.
-template <int BN>
+// and value halves per wave column (WCOLS of them, C = BN/WCOLS rows each):
+// rows [wn*C, wn*C + C/2) are gate rows col0 + wn*C/2 + w, the next C/2 are
+// the value rows f + the same.
+template <int BN, int WCOLS>
 struct MapGateValue {
   int64_t col0, f;
   __device__ __forceinline__ int64_t operator()(int r) const {
-    constexpr int kHalf = BN / 2, kQuarter = BN / 4;
-    const int wn = r / kHalf, w = r % kHalf;
-    return w < kQuarter ? col0 + wn * kQuarter + w : f + col0 + wn * kQuarter + (w - kQuarter);
+    constexpr int kCol = BN / WCOLS, kHalf = kCol / 2;
+    const int wn = r / kCol, w = r % kCol;
+    return w < kHalf ? col0 + wn * kHalf + w : f + col0 + wn * kHalf + (w - kHalf);
   }
 };
 
@@ -142,9 +144,9 @@ struct MapGateValue {
 // or 32 k rows of ROWS halves), i.e. ROWS / 16 wave instructions, ROWS / 64
 // per wave.  Per-lane source offsets are fixed; each stage adds a constant.
 // ---------------------------------------------------------------------------
-template <bool RC, int ROWS>
+template <bool RC, int ROWS, int WAVES>
 struct Dma {
-  static constexpr int kPerWave = ROWS / 64;
+  static constexpr int kPerWave = ROWS / 16 / WAVES;
   uint32_t off[kPerWave];  // byte offset of this lane's chunk at k = 0 of the kernel's range
   uint32_t kstep;          // bytes per stage
   __amdgpu_buffer_rsrc_t rsrc;
@@ -159,7 +161,7 @@ struct Dma {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int it = 0; it < kPerWave; ++it) {
-      const int b = (it * 4 + wave) * 1024 + lane * 16;
+      const int b = (it * WAVES + wave) * 1024 + lane * 16;
       const int row = b >> 6, chunk = ((b >> 4) & 3) ^ f_kc(row);
       off[it] = (uint32_t)((map(row) * ld + kbeg + chunk * 8) * 2);
     }
@@ -173,7 +175,7 @@ struct Dma {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int it = 0; it < kPerWave; ++it) {
-      const int b = (it * 4 + wave) * 1024 + lane * 16;
+      const int b = (it * WAVES + wave) * 1024 + lane * 16;
       const int krow = b / (ROWS * 2), chunk = ((b % (ROWS * 2)) >> 4) ^ f_rc<ROWS>(krow);
       off[it] = (uint32_t)(((kbeg + krow) * ld + row0 + chunk * 8) * 2);
     }
@@ -186,7 +188,7 @@ struct Dma {
     const int wave = threadIdx.x >> 6;
     const uint32_t voff = live ? off[it] + (uint32_t)st * kstep : 0x80000000u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rsrc, (RV_LDS void*)(lds + (it * 4 + wave) * 512), 16, voff, 0, 0, 0);
+        rsrc, (RV_LDS void*)(lds + (it * WAVES + wave) * 512), 16, voff, 0, 0, 0);
   }
   // Issue stage `st` (relative to the kernel's first k) into the tile at `lds`.
   __device__ __forceinline__ void issue(_Float16* lds, int st) const {
@@ -194,7 +196,7 @@ struct Dma {
 #pragma unroll
     for (int it = 0; it < kPerWave; ++it)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, (RV_LDS void*)(lds + (it * 4 + wave) * 512), 16, off[it] + (uint32_t)st * kstep,
+          rsrc, (RV_LDS void*)(lds + (it * WAVES + wave) * 512), 16, off[it] + (uint32_t)st * kstep,
           0, 0, 0);
   }
 };
@@ -284,18 +286,20 @@ __device__ __forceinline__ void tile_of(int64_t t, int64_t tiles_m, int64_t tile
   tn = r / gm;
 }
 
-template <int BM, int BN, bool A_RC, bool B_RC, Epi EPI>
-__global__ __launch_bounds__(kThreads)
+template <int BM, int BN, bool A_RC, bool B_RC, Epi EPI, int WAVES>
+__global__ __launch_bounds__(WAVES * 64)
 void gemm_kernel(GemmArgs args) {
-  constexpr int TM = BM / 64, TN = BN / 64;
+  // waves: 2 rows x WCOLS columns, each owning a WM x WN block of the tile
+  constexpr int WCOLS = WAVES / 2, WM = BM / 2, WN = BN / WCOLS;
+  constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int kStages = stages_for(BM, BN);
   constexpr int kA = BM * kBK, kB = BN * kBK;          // halves per stage and operand
   constexpr int kRing = kStages * (kA + kB);
-  constexpr int kStaging = 4 * (BM / 2) * (BN / 2 + 8);  // fp16 epilogue staging
+  constexpr int kStaging = WAVES * WM * (WN + 8);  // fp16 epilogue staging
   __shared__ __attribute__((aligned(16))) _Float16 lds[kRing > kStaging ? kRing : kStaging];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WCOLS, wn = wave % WCOLS;
 
   const int64_t tiles = args.tiles_m * args.tiles_n;
   const int64_t split = blockIdx.x / tiles;
@@ -307,13 +311,13 @@ void gemm_kernel(GemmArgs args) {
   const int64_t kend = kbeg + args.k_chunk < args.k ? kbeg + args.k_chunk : args.k;
   const int stages = kend > kbeg ? (int)((kend - kbeg + kBK - 1) / kBK) : 0;
 
-  Dma<A_RC, BM> da;
-  Dma<B_RC, BN> db;
+  Dma<A_RC, BM, WAVES> da;
+  Dma<B_RC, BN, WAVES> db;
   if constexpr (A_RC) da.init_rc(args.a, args.a_bytes, args.lda, m0, kbeg);
   else da.init_kc(args.a, args.a_bytes, args.lda, MapDirect{m0, args.m}, kbeg);
   if constexpr (B_RC) db.init_rc(args.b, args.b_bytes, args.ldb, n0, kbeg);
   else if constexpr (EPI == Epi::SwiGLU)
-    db.init_kc(args.b, args.b_bytes, args.ldb, MapGateValue<BN>{n0, args.f}, kbeg);
+    db.init_kc(args.b, args.b_bytes, args.ldb, MapGateValue<BN, WCOLS>{n0, args.f}, kbeg);
   else db.init_kc(args.b, args.b_bytes, args.ldb, MapDirect{n0, args.n}, kbeg);
 
   f32x16 acc[TM][TN];
@@ -337,14 +341,15 @@ void gemm_kernel(GemmArgs args) {
   // the buffer's range: it reads nothing from memory and writes zeros into a
   // buffer no later stage uses, and every iteration waits for the same
   // vmcnt.  Fragments prefetched past the last stage are never used.
-  constexpr int kPerWaveA = Dma<A_RC, BM>::kPerWave, kPerWave = kPerWaveA + Dma<B_RC, BN>::kPerWave;
+  constexpr int kPerWaveA = Dma<A_RC, BM, WAVES>::kPerWave;
+  constexpr int kPerWave = kPerWaveA + Dma<B_RC, BN, WAVES>::kPerWave;
   constexpr int kM = TM * TN, kF = TM + TN;
   f16x8 fa[2][TM], fb[2][TN];
 
 #define RV_FRAG(SLOT, LA, LB, KS, P)                                                        \
   do {                                                                                      \
-    if ((P) < TM) fa[SLOT][(P)] = frag<A_RC, BM>((LA), wm * (BM / 2) + (P) * 32, (KS), lane); \
-    else fb[SLOT][(P) - TM] = frag<B_RC, BN>((LB), wn * (BN / 2) + ((P) - TM) * 32, (KS), lane); \
+    if ((P) < TM) fa[SLOT][(P)] = frag<A_RC, BM>((LA), wm * WM + (P) * 32, (KS), lane);     \
+    else fb[SLOT][(P) - TM] = frag<B_RC, BN>((LB), wn * WN + ((P) - TM) * 32, (KS), lane);  \
   } while (0)
 #define RV_DMA(D, BUF, ST, LIVE)                                                            \
   do {                                                                                      \
@@ -413,13 +418,13 @@ void gemm_kernel(GemmArgs args) {
     // fp32 outputs: 16-byte stores straight from the accumulators.
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int64_t row = m0 + wm * (BM / 2) + i * 32 + (lane & 31);
+      const int64_t row = m0 + wm * WM + i * 32 + (lane & 31);
       if (row >= args.m) continue;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int64_t col = n0 + wn * (BN / 2) + j * 32 + q * 8 + cq;
+          const int64_t col = n0 + wn * WN + j * 32 + q * 8 + cq;
           const float a0 = acc[i][j][q * 4], a1 = acc[i][j][q * 4 + 1];
           const float a2 = acc[i][j][q * 4 + 2], a3 = acc[i][j][q * 4 + 3];
           if constexpr (EPI == Epi::PartialF32) {
@@ -442,10 +447,10 @@ void gemm_kernel(GemmArgs args) {
       }
     }
   } else {
-    // fp16 outputs: each wave stages fp16(acc) for its (BM/2) x (BN/2) tile
-    // in LDS (row stride WN + 8 halves), then moves whole rows, 16 bytes per
-    // lane, so every global access instruction covers full row segments.
-    constexpr int WM = BM / 2, WN = BN / 2, S = WN + 8;
+    // fp16 outputs: each wave stages fp16(acc) for its WM x WN block in LDS
+    // (row stride WN + 8 halves), then moves whole rows, 16 bytes per lane,
+    // so every global access instruction covers full row segments.
+    constexpr int S = WN + 8;
     _Float16* stage = lds + wave * (WM * S);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -533,35 +538,42 @@ void gemm_kernel(GemmArgs args) {
 // host dispatch can launch.  Without them this compiler emits the host-side
 // launch stubs of only some of the kernels reached through the dispatch
 // switch, and the library fails to load with undefined symbols.
-template __global__ void gemm_kernel<256, 256, false, false, Epi::SwiGLU>(GemmArgs);
-template __global__ void gemm_kernel<256, 256, false, false, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<256, 256, false, true, Epi::SwiGLUBwd>(GemmArgs);
-template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<256, 256, true, true, Epi::AccF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<256, 256, true, true, Epi::PartialF32>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, false, false, Epi::SwiGLU>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, false, false, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, false, true, Epi::SwiGLUBwd>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, false, true, Epi::StoreF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, true, true, Epi::AccF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, true, true, Epi::PartialF32>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, false, false, Epi::SwiGLU>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, false, false, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, false, true, Epi::SwiGLUBwd>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, false, true, Epi::StoreF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, true, true, Epi::AccF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, true, true, Epi::PartialF32>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, false, false, Epi::SwiGLU>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, false, false, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, false, true, Epi::SwiGLUBwd>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, true, true, Epi::AccF32OfF16>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, true, true, Epi::PartialF32>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, false, Epi::SwiGLU, 4>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, false, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::SwiGLUBwd, 4>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, true, true, Epi::AccF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, true, true, Epi::PartialF32, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, false, Epi::SwiGLU, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, false, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, true, Epi::SwiGLUBwd, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, true, Epi::StoreF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, true, true, Epi::AccF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, true, true, Epi::PartialF32, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, false, Epi::SwiGLU, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, false, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, true, Epi::SwiGLUBwd, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, true, Epi::StoreF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, true, true, Epi::AccF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, true, true, Epi::PartialF32, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, false, Epi::SwiGLU, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, false, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, true, Epi::SwiGLUBwd, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, true, true, Epi::AccF32OfF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, true, true, Epi::PartialF32, 4>(GemmArgs);
 
-template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 256, false, true, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<128, 128, false, true, Epi::StoreF16>(GemmArgs);
-template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF16>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 256, false, true, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<128, 128, false, true, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<64, 128, false, true, Epi::StoreF16, 4>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, false, Epi::SwiGLU, 8>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, false, Epi::StoreF16, 8>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::SwiGLUBwd, 8>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF32OfF16, 8>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, true, true, Epi::AccF32OfF16, 8>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, true, true, Epi::PartialF32, 8>(GemmArgs);
+template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF16, 8>(GemmArgs);
 
 // acc[i] (+)= fp32(fp16(sum_s part[s][i])), splits summed in order.  This is
 // autocast's weight gradient: the fp16 GEMM result, cast to the fp32 weight
@@ -612,18 +624,24 @@ void cast_f32_f16(const float* __restrict__ src, __half* __restrict__ dst, int64
 // Host side: tile-shape choice and launches.
 // ---------------------------------------------------------------------------
 struct TileShape {
-  int bm, bn;
+  int bm, bn, waves;
 };
-constexpr TileShape kShapes[4] = {{256, 256}, {128, 256}, {128, 128}, {64, 128}};
+// The first kRuleShapes are the ones pick_act's rule and the weight-gradient
+// plan choose from; the tuner also times the rest (256 x 256 with 8 waves:
+// two waves per SIMD, each owning a 128 x 64 block).
+constexpr int kNumShapes = 5, kRuleShapes = 4;
+constexpr TileShape kShapes[kNumShapes] = {
+    {256, 256, 4}, {128, 256, 4}, {128, 128, 4}, {64, 128, 4}, {256, 256, 8}};
 
 template <bool A_RC, bool B_RC, Epi EPI>
 int launch(int shape, const GemmArgs& a, int64_t splits, hipStream_t s) {
-  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * splits)), block(kThreads);
+  const dim3 grid((unsigned)(a.tiles_m * a.tiles_n * splits)), block(kShapes[shape].waves * 64);
   switch (shape) {
-    case 0: hipLaunchKernelGGL((gemm_kernel<256, 256, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
-    case 1: hipLaunchKernelGGL((gemm_kernel<128, 256, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((gemm_kernel<128, 128, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((gemm_kernel<64, 128, A_RC, B_RC, EPI>), grid, block, 0, s, a); break;
+    case 0: hipLaunchKernelGGL((gemm_kernel<256, 256, A_RC, B_RC, EPI, 4>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((gemm_kernel<128, 256, A_RC, B_RC, EPI, 4>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((gemm_kernel<128, 128, A_RC, B_RC, EPI, 4>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((gemm_kernel<64, 128, A_RC, B_RC, EPI, 4>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<256, 256, A_RC, B_RC, EPI, 8>), grid, block, 0, s, a); break;
   }
   return rv_host::check_launch();
 }
@@ -634,7 +652,7 @@ int launch(int shape, const GemmArgs& a, int64_t splits, hipStream_t s) {
 int pick_act(int64_t m, int64_t n_cols, bool swiglu) {
   int best = -1;
   int64_t best_blocks = -1;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kRuleShapes; ++i) {
     const int64_t cols = swiglu ? kShapes[i].bn / 2 : kShapes[i].bn;
     if (n_cols % cols) continue;
     const int64_t blocks = ((m + kShapes[i].bm - 1) / kShapes[i].bm) * (n_cols / cols);
@@ -657,6 +675,7 @@ int pick_act(int64_t m, int64_t n_cols, bool swiglu) {
 // (that would synchronise): it takes the shape already chosen for its key,
 // else pick_act's rule.  RV_GEMM_TUNE=0 in the environment turns tuning off.
 using TuneKey = std::tuple<int, int, int, int64_t, int64_t, int64_t>;
+std::atomic<int> g_forced_shape{-1};  // rv_gemm_force_shape; -1: measured / rule choice
 std::mutex g_tune_mu;
 std::map<TuneKey, int> g_tuned;
 
@@ -695,7 +714,7 @@ int tune_act(const GemmArgs& a, int64_t n_cols, hipStream_t s, int fallback) {
   }
   int best = fallback;
   float best_ms = 0.f;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kNumShapes; ++i) {
     const int64_t cols = swiglu ? kShapes[i].bn / 2 : kShapes[i].bn;
     if (n_cols % cols) continue;
     if (launch_shape<A_RC, B_RC, EPI>(i, a, n_cols, s) != RV_OK) continue;
@@ -717,6 +736,11 @@ int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
   const bool swiglu = EPI == Epi::SwiGLU;
   int shape = pick_act(a.m, n_cols, swiglu);
   if (shape < 0) return RV_ERR_UNSUPPORTED;
+  const int forced = g_forced_shape.load();
+  if (forced >= 0) {
+    if (n_cols % (swiglu ? kShapes[forced].bn / 2 : kShapes[forced].bn)) return RV_ERR_UNSUPPORTED;
+    return launch_shape<A_RC, B_RC, EPI>(forced, a, n_cols, s);
+  }
   if (tuning_enabled()) {
     int device = 0;
     (void)hipGetDevice(&device);
@@ -744,10 +768,10 @@ struct WgradPlan {
   int64_t tiles_m, tiles_n, splits, chunk;
 };
 WgradPlan plan_wgrad(int64_t rows, int64_t ni, int64_t nj) {
-  static const double eff[4] = {0.8, 0.7, 0.5, 0.35};
+  static const double eff[kRuleShapes] = {0.8, 0.7, 0.5, 0.35};
   WgradPlan best{-1, 0, 0, 0, 0};
   double best_cost = 0;
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kRuleShapes; ++i) {
     const TileShape t = kShapes[i];
     if (ni % t.bm || nj % t.bn) continue;
     const int64_t tiles = (ni / t.bm) * (nj / t.bn);
@@ -808,6 +832,14 @@ bool fits32(int64_t elems) { return elems > 0 && elems * 2 <= (int64_t)INT32_MAX
 }  // namespace
 
 extern "C" {
+
+int rv_gemm_num_shapes(void) { return kNumShapes; }
+
+int rv_gemm_force_shape(int shape) {
+  if (shape < -1 || shape >= kNumShapes) return RV_ERR_BAD_SIZE;
+  g_forced_shape.store(shape);
+  return RV_OK;
+}
 
 int rv_cast_f32_f16(const float* src, void* dst, int64_t n, void* stream) {
   if (!src || !dst) return RV_ERR_NULL_POINTER;

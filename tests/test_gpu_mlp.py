@@ -12,10 +12,11 @@ plus relative-L2 agreement (1e-3).  The SwiGLU parts are checked against the
 CPU oracle applied to the kernel's own pre-activations.  The bound is in
 tests/gemm_bounds.py.
 
-The shapes make every tile shape the library chooses (256x256, 128x256,
-128x128, 64x128) serve every epilogue at least once, and the weight gradients
-take both the direct-accumulate and the split-K path; the 8192 x 1024 x 4096
-case is one configs[4] token tile.
+The activation GEMMs take the fastest tile shape measured on their first call;
+test_every_tile_shape_gives_identical_bits forces each shape in turn
+(rv_gemm_force_shape) so that every shape serves every epilogue, and the
+weight gradients take both the direct-accumulate and the split-K path; the
+8192 x 1024 x 4096 case is one configs[4] token tile.
 """
 from __future__ import annotations
 
@@ -139,3 +140,48 @@ def test_rejects_fp32_operands(cuda_device):
         mlp.up_swiglu(x, mlp.cast_f16(up))
     with pytest.raises(ValueError, match="fp16"):
         mlp.up_swiglu(x.half(), up)
+
+
+@pytest.mark.parametrize("rows,d,f", [(1000, 256, 1024), (2100, 1024, 4096)])
+def test_every_tile_shape_gives_identical_bits(cuda_device, rows, d, f):
+    """The activation GEMMs sum each output's k blocks in the same order in
+    every tile shape (rv_gemm_force_shape; the default picks the fastest), so
+    every shape -- 4-wave 256x256 / 128x256 / 128x128 / 64x128 and the 8-wave
+    256x256 -- gives the same bits, ragged row tails included; shape 0's
+    results also meet the fp64 bound."""
+    from reversability_amd._hip import RV_F32, _stream, library
+    lib = library()
+    up, down = weights(d, f, cuda_device)
+    up16, down16 = mlp.cast_f16(up), mlp.cast_f16(down)
+    g = torch.Generator().manual_seed(7)
+    x16 = torch.randn(rows, d, generator=g).half().to(cuda_device)
+    dy = torch.randn(rows, d, generator=g).half().to(cuda_device)
+    wq = (0.02 * torch.randn(3 * d, d, generator=g)).half().to(cuda_device)
+    gq = torch.randn(rows, 3 * d, generator=g).half().to(cuda_device)
+
+    def run():
+        o, u = mlp.up_swiglu(x16, up16, keep_u=True)
+        y = mlp.down(o, down16, torch.empty(rows, d, device=cuda_device, dtype=torch.float16))
+        du = mlp.dgate(dy, down16, u)
+        dx = mlp.dx(du, up16, torch.empty(rows, d, device=cuda_device))
+        q = torch.empty(rows, 3 * d, device=cuda_device, dtype=torch.float16)
+        assert lib.rv_linear_fwd(x16.data_ptr(), d, wq.data_ptr(), rows, d, 3 * d, q.data_ptr(),
+                                 _stream(x16)) == 0
+        dq = torch.empty(rows, d, device=cuda_device)
+        assert lib.rv_linear_dx(gq.data_ptr(), wq.data_ptr(), rows, d, 3 * d, dq.data_ptr(),
+                                RV_F32, _stream(x16)) == 0
+        torch.cuda.synchronize()
+        return {"o": o, "u": u, "y": y, "du": du, "dx": dx, "q": q, "dq": dq}
+
+    results = []
+    try:
+        for shape in range(lib.rv_gemm_num_shapes()):
+            assert lib.rv_gemm_force_shape(shape) == 0
+            results.append(run())
+    finally:
+        assert lib.rv_gemm_force_shape(-1) == 0
+    for shape, res in enumerate(results[1:], 1):
+        for k, v in res.items():
+            assert torch.equal(v, results[0][k]), (shape, k)
+    assert within_gemm_bound(results[0]["q"], x16, wq, d)
+    assert lib.rv_gemm_force_shape(lib.rv_gemm_num_shapes()) != 0
