@@ -189,6 +189,14 @@ int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
  * (src/reversibility/optimized_v3.py:15-17 under torch.autocast). */
 int rv_cast_f32_f16(const float* src, void* dst, int64_t n, void* stream);
 
+/* The same cast for count <= rv_cast_f32_f16_max_tensors() tensors in one
+ * launch (dst[i][j] = fp16(src[i][j]), j < numel[i]; 16-byte aligned
+ * pointers): all of a step's weight casts at once instead of one launch per
+ * weight and evaluation. */
+int rv_cast_f32_f16_max_tensors(void);
+int rv_cast_f32_f16_multi(int count, const float* const* src, void* const* dst,
+                          const int64_t* numel, void* stream);
+
 /* o[rows, f] = fp16(silu(fp16(u_g))) * fp16(u_v), u = x W_up^T; x fp16 with
  * row stride ldx, w_up fp16 [2f, d].  If u is not NULL the fp16
  * pre-activation u[rows, 2f] = [u_g | u_v] is written too. */

@@ -51,6 +51,8 @@ SIGNATURES = {
     "rv_residual_axpy": (_I, [_P, _P, _P, _I, _I64, _I, _I, _P]),
     "rv_add_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_cast_f32_f16": (_I, [_P, _P, _I64, _P]),
+    "rv_cast_f32_f16_max_tensors": (_I, []),
+    "rv_cast_f32_f16_multi": (_I, [_I, _P, _P, _P, _P]),
     "rv_linear_fwd": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P]),
     "rv_linear_dx": (_I, [_P, _P, _I64, _I64, _I64, _P, _I, _P]),
     "rv_linear_dw_workspace_bytes": (_I64, [_I64, _I64, _I64]),

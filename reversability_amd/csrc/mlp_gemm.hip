@@ -621,6 +621,48 @@ void cast_f32_f16(const float* __restrict__ src, __half* __restrict__ dst, int64
   }
 }
 
+// dst[t] = fp16(src[t]) for up to kCastTensors tensors in one launch: the
+// pointer table and per-tensor chunk prefix sums travel in the kernel
+// arguments; each workgroup casts one kCastChunk-element chunk of one tensor
+// with cast_f32_f16's arithmetic.
+constexpr int kCastTensors = 64;
+constexpr int64_t kCastChunk = 256 * 8 * 16;
+struct CastTable {
+  const float* src[kCastTensors];
+  __half* dst[kCastTensors];
+  int64_t n[kCastTensors];
+  int chunk_start[kCastTensors + 1];
+  int count;
+};
+
+__global__ __launch_bounds__(256)
+void cast_multi_k(CastTable tab) {
+  int t = 0;
+  for (int i = 1; i < tab.count; ++i)
+    if (tab.chunk_start[i] <= (int)blockIdx.x) t = i;
+  const int64_t base = (int64_t)(blockIdx.x - tab.chunk_start[t]) * kCastChunk;
+  const int64_t n = tab.n[t];
+  const float* src = tab.src[t];
+  __half* dst = tab.dst[t];
+  const int64_t end = base + kCastChunk < n ? base + kCastChunk : n;
+  for (int64_t i = base + threadIdx.x * 8; i < end; i += 256 * 8) {
+    if (i + 8 <= end) {
+      const float4 a = *reinterpret_cast<const float4*>(src + i);
+      const float4 b = *reinterpret_cast<const float4*>(src + i + 4);
+      const __half2 h0 = __floats2half2_rn(a.x, a.y), h1 = __floats2half2_rn(a.z, a.w);
+      const __half2 h2 = __floats2half2_rn(b.x, b.y), h3 = __floats2half2_rn(b.z, b.w);
+      uint4 v;
+      v.x = *reinterpret_cast<const uint32_t*>(&h0);
+      v.y = *reinterpret_cast<const uint32_t*>(&h1);
+      v.z = *reinterpret_cast<const uint32_t*>(&h2);
+      v.w = *reinterpret_cast<const uint32_t*>(&h3);
+      *reinterpret_cast<uint4*>(dst + i) = v;
+    } else {
+      for (int64_t j = i; j < end; ++j) dst[j] = __float2half_rn(src[j]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side: tile-shape choice and launches.
 // ---------------------------------------------------------------------------
@@ -851,6 +893,34 @@ int rv_cast_f32_f16(const float* src, void* dst, int64_t n, void* stream) {
   if (blocks > 8 * kCUs) blocks = 8 * kCUs;
   hipLaunchKernelGGL(cast_f32_f16, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, src,
                      static_cast<__half*>(dst), n);
+  return rv_host::check_launch();
+}
+
+int rv_cast_f32_f16_max_tensors(void) { return kCastTensors; }
+
+int rv_cast_f32_f16_multi(int count, const float* const* src, void* const* dst,
+                          const int64_t* numel, void* stream) {
+  if (count < 0) return RV_ERR_BAD_SIZE;
+  if (count == 0) return RV_OK;
+  if (!src || !dst || !numel) return RV_ERR_NULL_POINTER;
+  if (count > kCastTensors) return RV_ERR_UNSUPPORTED;
+  CastTable tab{};
+  int64_t chunks = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!src[i] || !dst[i]) return RV_ERR_NULL_POINTER;
+    if (numel[i] < 0) return RV_ERR_BAD_SIZE;
+    if (!ok16(src[i]) || !ok16(dst[i])) return RV_ERR_UNSUPPORTED;
+    tab.src[i] = src[i];
+    tab.dst[i] = static_cast<__half*>(dst[i]);
+    tab.n[i] = numel[i];
+    tab.chunk_start[i] = (int)chunks;
+    chunks += (numel[i] + kCastChunk - 1) / kCastChunk;
+    if (chunks > 0x7fffffff) return RV_ERR_UNSUPPORTED;
+  }
+  tab.chunk_start[count] = (int)chunks;
+  tab.count = count;
+  if (chunks == 0) return RV_OK;
+  hipLaunchKernelGGL(cast_multi_k, dim3((unsigned)chunks), dim3(256), 0, (hipStream_t)stream, tab);
   return rv_host::check_launch();
 }
 

@@ -100,3 +100,4 @@ def enable_linear(model: torch.nn.Module) -> None:
     for block in model.blocks:
         for layer in (block.attn.qkv, block.attn.proj):
             layer.forward = types.MethodType(forward, layer)
+            layer._rv_linear = True  # its weight is cast by mlp.cast_weight

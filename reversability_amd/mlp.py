@@ -20,6 +20,7 @@ torch's GEMMs otherwise.
 from __future__ import annotations
 
 import contextlib
+import ctypes
 
 import torch
 
@@ -86,6 +87,43 @@ def cast_weight(w: torch.Tensor) -> torch.Tensor:
     w16 = cast_f16(w)
     cache[id(w)] = (w, w16)  # the strong reference keeps id(w) unique in the block
     return w16
+
+
+def prefetch_casts(weights) -> None:
+    """Inside a ``weight_cast_cache`` block, make the fp16 casts of all of
+    ``weights`` (contiguous fp32 CUDA tensors; others are skipped) in one
+    launch per rv_cast_f32_f16_max_tensors() tensors, into one buffer, so
+    that the block's ``cast_weight`` calls find them.  Same values as
+    ``cast_f16`` per weight.  No effect outside a block."""
+    cache = _weight_cache
+    if cache is None:
+        return
+    todo, seen = [], set()
+    for w in weights:
+        if (w.is_cuda and w.dtype == torch.float32 and w.is_contiguous() and w.numel()
+                and id(w) not in cache and id(w) not in seen):
+            todo.append(w)
+            seen.add(id(w))
+    if not todo:
+        return
+    lib = library()
+    limit = lib.rv_cast_f32_f16_max_tensors()
+    for start in range(0, len(todo), limit):
+        group = todo[start:start + limit]
+        sizes = [-(-w.numel() // 8) * 8 for w in group]  # 16-byte aligned slices
+        flat = torch.empty(sum(sizes), device=group[0].device, dtype=torch.float16)
+        outs, offset = [], 0
+        for w, size in zip(group, sizes):
+            outs.append(flat[offset:offset + w.numel()].view(w.shape))
+            offset += size
+        n = len(group)
+        src = (ctypes.c_void_p * n)(*[w.data_ptr() for w in group])
+        dst = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        numel = (ctypes.c_int64 * n)(*[w.numel() for w in group])
+        _check(lib.rv_cast_f32_f16_multi(n, src, dst, numel, _stream(group[0])),
+               "rv_cast_f32_f16_multi")
+        for w, o in zip(group, outs):
+            cache[id(w)] = (w, o)
 
 
 def _f16(t: torch.Tensor, what: str) -> None:

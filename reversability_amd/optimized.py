@@ -100,8 +100,11 @@ def chunked_backward(model, ids, labels, denominator, chunk_tokens, scaler=None,
     """
     if chunk_tokens <= 0 or denominator <= 0:
         raise ValueError("Chunk size and normalization denominator must be positive")
-    from .mlp import weight_cast_cache
+    from .mlp import prefetch_casts, weight_cast_cache
+    from .optimized_v3 import castable_weights
     with weight_cast_cache():  # weights are constant until the optimizer step
+        if precision == "fp16" and ids.device.type == "cuda":
+            prefetch_casts(castable_weights(model))
         return _chunked_backward(model, ids, labels, denominator, chunk_tokens, scaler,
                                  precision, reuse, loss_backend)
 

@@ -358,8 +358,27 @@ def cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler=N
         raise ValueError("Use installed core mode and positive normalization/chunk")
     from . import mlp
     with mlp.weight_cast_cache():  # weights are constant until the optimizer step
+        if precision == "fp16" and ids.device.type == "cuda":
+            mlp.prefetch_casts(castable_weights(model))
         return _cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler,
                                      precision, loss_backend)
+
+
+def castable_weights(model) -> list:
+    """The fp32 weights the step's MFMA GEMMs cast to fp16 through
+    ``mlp.cast_weight``: the tiled MLP's up and down projections when
+    ``install_v3`` tiled the MLP, the attention projections routed through
+    ``linear.enable_linear``.  One ``mlp.prefetch_casts`` launch makes all of
+    them at the start of a step."""
+    tiled = bool(getattr(model, "_v3_signature", (None, 0))[1])
+    weights = []
+    for block in model.blocks:
+        for layer in (block.attn.qkv, block.attn.proj):
+            if getattr(layer, "_rv_linear", False):
+                weights.append(layer.weight)
+        if tiled:
+            weights += [block.mlp.up.weight, block.mlp.down.weight]
+    return weights
 
 
 def _cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler, precision,

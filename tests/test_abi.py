@@ -129,3 +129,21 @@ def test_fused_cross_entropy_validates_without_device():
     assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 65544, 4, 65544, fake)) == 3  # too wide
     # logits and dlogits must share their address modulo 16
     assert lib.rv_ce_fused(*args(fake, _hip.RV_F16, 8, 4, 8, ctypes.c_void_p(4098))) == 3
+
+
+def test_multi_cast_validates_without_device():
+    lib = _hip.library()
+    n = lib.rv_cast_f32_f16_max_tensors()
+    assert n >= 32
+    fake = ctypes.c_void_p(4096)
+    P = ctypes.c_void_p * 2
+    numel = (ctypes.c_int64 * 2)(8, 8)
+    assert lib.rv_cast_f32_f16_multi(0, None, None, None, None) == 0
+    assert lib.rv_cast_f32_f16_multi(-1, None, None, None, None) == 2
+    assert lib.rv_cast_f32_f16_multi(2, None, P(fake, fake), numel, None) == 1
+    assert lib.rv_cast_f32_f16_multi(2, P(fake, None), P(fake, fake), numel, None) == 1
+    assert lib.rv_cast_f32_f16_multi(2, P(fake, fake), P(fake, ctypes.c_void_p(4098)), numel,
+                                     None) == 3  # 16-byte alignment
+    assert lib.rv_cast_f32_f16_multi(n + 1, P(fake, fake), P(fake, fake), numel, None) == 3
+    bad = (ctypes.c_int64 * 2)(8, -1)
+    assert lib.rv_cast_f32_f16_multi(2, P(fake, fake), P(fake, fake), bad, None) == 2

@@ -185,3 +185,24 @@ def test_every_tile_shape_gives_identical_bits(cuda_device, rows, d, f):
             assert torch.equal(v, results[0][k]), (shape, k)
     assert within_gemm_bound(results[0]["q"], x16, wq, d)
     assert lib.rv_gemm_force_shape(lib.rv_gemm_num_shapes()) != 0
+
+
+def test_multi_tensor_cast_and_prefetch(cuda_device):
+    """rv_cast_f32_f16_multi equals rv_cast_f32_f16 per tensor, bit for bit
+    (ragged sizes, more tensors than one launch takes); prefetch_casts fills
+    the weight-cast cache with those values, and cast_weight hands them out."""
+    g = torch.Generator().manual_seed(3)
+    sizes = [(1,), (7,), (8,), (1001,), (256, 768), (4096, 1024), (33, 65)] * 10
+    ws = [(70000 * torch.randn(*s, generator=g)).to(cuda_device) for s in sizes]  # some overflow
+    with mlp.weight_cast_cache():
+        mlp.prefetch_casts(ws)
+        got = [mlp.cast_weight(w) for w in ws]
+        cache = mlp._weight_cache
+        assert all(cache[id(w)][1] is c for w, c in zip(ws, got))
+    for w, c in zip(ws, got):
+        ref = mlp.cast_f16(w)
+        assert c.shape == w.shape and c.dtype == torch.float16
+        assert torch.equal(c.view(torch.int16), ref.view(torch.int16))
+    # outside a block it does nothing
+    mlp.prefetch_casts(ws)
+    assert mlp._weight_cache is None
