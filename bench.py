@@ -300,8 +300,7 @@ def make_train_step(dev, name: str):
         opt.zero_grad(set_to_none=True)
         loss = cached_head_backward(model, x, y, targets, HEAD_CHUNK or targets, scaler, "fp16",
                                     False, "triton")
-        scaler.unscale_(opt)
-        torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0)
+        opt.unscale_clip_(scaler, 1.0)  # scaler.unscale_(opt) + clip_grad_norm_(params, 1.0)
         scaler.step(opt)
         scaler.update()
         return loss

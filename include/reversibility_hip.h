@@ -292,6 +292,34 @@ int rv_adamw_step(int count, float* const* params, const float* const* grads,
                   double eps, double weight_decay, const float* step,
                   const float* found_inf, const float* inv_scale, void* stream);
 
+/* rv_adamw_step with clip_grad_norm_'s multiply as well: g times *inv_scale
+ * (if given), rounded, times *clip_coef (if given), rounded -- the values
+ * GradScaler.unscale_ and clip_grad_norm_ would have written into the
+ * gradients -- so those two passes need not write them. */
+int rv_adamw_step_clipped(int count, float* const* params, const float* const* grads,
+                          float* const* exp_avg, float* const* exp_avg_sq,
+                          const int64_t* numel, double lr, double beta1, double beta2,
+                          double eps, double weight_decay, const float* step,
+                          const float* found_inf, const float* inv_scale,
+                          const float* clip_coef, void* stream);
+
+/* GradScaler.unscale_ followed by torch.nn.utils.clip_grad_norm_(params,
+ * max_norm) (norm type 2; scripts/train_baseline.py:278-280) without writing
+ * the gradients: rv_grad_sq_partials stores, for each 65536-element chunk of
+ * each of count <= rv_adamw_max_tensors() gradients, the fp32 sum of squares
+ * of g * *inv_scale (inv_scale nullable) and a non-finite flag at index
+ * first + chunk of partials / flags (rv_grad_chunks(numel, count) chunks; a
+ * negative return is -status); rv_grad_clip_coef reduces n partials in a
+ * fixed order to total_norm = sqrt(sum), clip_coef = min(max_norm /
+ * (total_norm + 1e-6), 1) and found_inf = 1 if any chunk was non-finite
+ * (0 otherwise), all device fp32 scalars for rv_adamw_step_clipped. */
+int rv_grad_chunks(const int64_t* numel, int count);
+int rv_grad_sq_partials(int count, const float* const* grads, const int64_t* numel,
+                        const float* inv_scale, float* partials, float* flags, int first,
+                        void* stream);
+int rv_grad_clip_coef(const float* partials, const float* flags, int n, double max_norm,
+                      float* total_norm, float* clip_coef, float* found_inf, void* stream);
+
 /* ------------------------------------------------------------------------
  * Cross-entropy over vocabulary rows (the tied LM head's loss).
  * logits [rows, ld] fp16 (RV_F16) or fp32 (RV_F32), first cols columns used;

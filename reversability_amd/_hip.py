@@ -60,6 +60,11 @@ SIGNATURES = {
     "rv_adamw_max_tensors": (_I, []),
     "rv_adamw_advance": (_I, [_P, _P, _P]),
     "rv_adamw_step": (_I, [_I, _P, _P, _P, _P, _P, _D, _D, _D, _D, _D, _P, _P, _P, _P]),
+    "rv_adamw_step_clipped": (_I, [_I, _P, _P, _P, _P, _P, _D, _D, _D, _D, _D, _P, _P, _P, _P,
+                                   _P]),
+    "rv_grad_chunks": (_I, [_P, _I]),
+    "rv_grad_sq_partials": (_I, [_I, _P, _P, _P, _P, _P, _I, _P]),
+    "rv_grad_clip_coef": (_I, [_P, _P, _I, _D, _P, _P, _P, _P]),
     "rv_ce_fwd": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "rv_ce_bwd": (_I, [_P, _I, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_gemm_num_shapes": (_I, []),

@@ -46,6 +46,7 @@ struct Hyper {
   const float* step;                   // t after this update (already advanced)
   const float* found_inf;              // nullable
   const float* inv_scale;              // nullable
+  const float* clip;                   // nullable: clip_grad_norm_'s clamped coefficient
 };
 
 // torch's lerp, addcmul and addcdiv as its ROCm build evaluates them: the
@@ -56,12 +57,13 @@ __device__ __forceinline__ float lerp_t(float a, float b, float w) {
 }
 
 struct Scalars {
-  float w1, one_minus_b2, step_size, bc2_sqrt, inv;
+  float w1, one_minus_b2, step_size, bc2_sqrt, inv, clip;
 };
 
 __device__ __forceinline__ void update1(float& p, float g, float& m, float& v, const Hyper& h,
                                         const Scalars& s) {
-  g = g * s.inv;
+  g = g * s.inv;   // GradScaler.unscale_ (exact when inv == 1)
+  g = g * s.clip;  // clip_grad_norm_'s multiply (exact when clip == 1)
   p = p * h.decay;
   m = lerp_t(m, g, s.w1);
   v = v * h.beta2;
@@ -86,6 +88,7 @@ void adamw_k(TensorTable tab, Hyper h) {
   s.step_size = (float)(h.lr_d / (1.0 - pow(h.beta1_d, step)));
   s.bc2_sqrt = (float)sqrt(1.0 - pow(h.beta2_d, step));
   s.inv = h.inv_scale != nullptr ? *h.inv_scale : 1.0f;
+  s.clip = h.clip != nullptr ? *h.clip : 1.0f;
   float* p = tab.p[t];
   const float* g = tab.g[t];
   float* m = tab.m[t];
@@ -114,6 +117,109 @@ void adamw_k(TensorTable tab, Hyper h) {
   }
 }
 
+// Gradient-norm pass of GradScaler.unscale_ + clip_grad_norm_(p, max_norm, 2):
+// per chunk of one tensor (same table and chunking as the update) the fp32 sum
+// of squares of the unscaled gradient g * inv (the value unscale_ would write)
+// and whether any unscaled element is non-finite.  Fixed summation order:
+// each thread its elements in order, then a wave butterfly, then the waves in
+// order.  Partials go to part[first + chunk], flags to flag[first + chunk].
+struct GradTable {
+  const float* g[kMaxTensors];
+  int64_t n[kMaxTensors];
+  int chunk_start[kMaxTensors + 1];
+  int count;
+};
+
+__global__ __launch_bounds__(kThreads)
+void grad_sq_k(GradTable tab, const float* __restrict__ inv_scale, float* __restrict__ part,
+               float* __restrict__ flag, int first) {
+  int t = 0;
+  for (int i = 1; i < tab.count; ++i)
+    if (tab.chunk_start[i] <= (int)blockIdx.x) t = i;
+  const int64_t off = (int64_t)(blockIdx.x - tab.chunk_start[t]) * kChunk;
+  const int64_t end = off + kChunk < tab.n[t] ? off + kChunk : tab.n[t];
+  const float inv = inv_scale != nullptr ? *inv_scale : 1.0f;
+  const float* g = tab.g[t];
+  float ss = 0.f;
+  bool bad = false;
+  auto add = [&](float x) {
+    const float u = x * inv;
+    bad = bad || !isfinite(u);
+    ss = __builtin_fmaf(u, u, ss);
+  };
+  int64_t i = off + threadIdx.x * 4;
+  if ((reinterpret_cast<uintptr_t>(g) & 15) == 0) {
+    for (; i + 4 <= end; i += kThreads * 4) {
+      const float4 q = *reinterpret_cast<const float4*>(g + i);
+      add(q.x);
+      add(q.y);
+      add(q.z);
+      add(q.w);
+    }
+    for (int64_t j = (i < end ? i : end); j < end; ++j) add(g[j]);
+  } else {
+    for (int64_t j = off + threadIdx.x; j < end; j += kThreads) add(g[j]);
+  }
+  ss = rv::wave_sum(ss);
+  const bool wave_bad = __any(bad);
+  __shared__ float ws[kThreads / 64];
+  __shared__ int wb[kThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    ws[wave] = ss;
+    wb[wave] = wave_bad;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float tot = ws[0];
+    int any = wb[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) {
+      tot = tot + ws[w];
+      any |= wb[w];
+    }
+    part[first + blockIdx.x] = tot;
+    flag[first + blockIdx.x] = any ? 1.0f : 0.0f;
+  }
+}
+
+// total = sqrt(sum of the partials, in order), clip = min(max_norm / (total +
+// 1e-6), 1) (clip_grad_norm_'s fp32 formulas), found_inf = 1 if any chunk had
+// a non-finite unscaled gradient.  One workgroup.
+__global__ __launch_bounds__(kThreads)
+void grad_clip_k(const float* __restrict__ part, const float* __restrict__ flag, int n,
+                 float max_norm, float* __restrict__ total, float* __restrict__ clip,
+                 float* __restrict__ found_inf) {
+  float ss = 0.f;
+  float any = 0.f;
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    ss = ss + part[i];
+    any = fmaxf(any, flag[i]);
+  }
+  ss = rv::wave_sum(ss);
+  for (int o = 32; o >= 1; o >>= 1) any = fmaxf(any, __shfl_xor(any, o, 64));
+  __shared__ float ws[kThreads / 64], wa[kThreads / 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    ws[wave] = ss;
+    wa[wave] = any;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float tot = ws[0], a = wa[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) {
+      tot = tot + ws[w];
+      a = fmaxf(a, wa[w]);
+    }
+    const float norm = sqrtf(tot);
+    const float coef = max_norm / (norm + 1e-6f);
+    *total = norm;
+    *clip = coef < 1.0f ? coef : 1.0f;
+    *found_inf = a;
+  }
+}
+
 __global__ void adamw_advance_k(float* step, const float* found_inf) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     if (found_inf == nullptr || *found_inf == 0.0f) *step = *step + 1.0f;
@@ -132,11 +238,66 @@ int rv_adamw_advance(float* step, const float* found_inf, void* stream) {
   return rv_host::check_launch();
 }
 
+int rv_grad_chunks(const int64_t* numel, int count) {
+  if (count < 0 || (count > 0 && !numel)) return -RV_ERR_BAD_SIZE;
+  int64_t chunks = 0;
+  for (int i = 0; i < count; ++i) {
+    if (numel[i] < 0) return -RV_ERR_BAD_SIZE;
+    chunks += (numel[i] + kChunk - 1) / kChunk;
+    if (chunks > 0x7fffffff) return -RV_ERR_UNSUPPORTED;
+  }
+  return (int)chunks;
+}
+
+int rv_grad_sq_partials(int count, const float* const* grads, const int64_t* numel,
+                        const float* inv_scale, float* partials, float* flags, int first,
+                        void* stream) {
+  if (count <= 0) return count == 0 ? RV_OK : RV_ERR_BAD_SIZE;
+  if (count > kMaxTensors) return RV_ERR_UNSUPPORTED;
+  if (!grads || !numel || !partials || !flags) return RV_ERR_NULL_POINTER;
+  if (first < 0) return RV_ERR_BAD_SIZE;
+  GradTable tab{};
+  int chunks = 0;
+  for (int i = 0; i < count; ++i) {
+    if (!grads[i]) return RV_ERR_NULL_POINTER;
+    if (numel[i] <= 0) return RV_ERR_BAD_SIZE;
+    tab.g[i] = grads[i];
+    tab.n[i] = numel[i];
+    tab.chunk_start[i] = chunks;
+    const int64_t c = (numel[i] + kChunk - 1) / kChunk;
+    if ((int64_t)chunks + c > 0x7fffffff) return RV_ERR_UNSUPPORTED;
+    chunks += (int)c;
+  }
+  tab.chunk_start[count] = chunks;
+  tab.count = count;
+  hipLaunchKernelGGL(grad_sq_k, dim3((unsigned)chunks), dim3(kThreads), 0, (hipStream_t)stream,
+                     tab, inv_scale, partials, flags, first);
+  return rv_host::check_launch();
+}
+
+int rv_grad_clip_coef(const float* partials, const float* flags, int n, double max_norm,
+                      float* total_norm, float* clip_coef, float* found_inf, void* stream) {
+  if (n <= 0) return RV_ERR_BAD_SIZE;
+  if (!partials || !flags || !total_norm || !clip_coef || !found_inf) return RV_ERR_NULL_POINTER;
+  hipLaunchKernelGGL(grad_clip_k, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, partials, flags,
+                     n, (float)max_norm, total_norm, clip_coef, found_inf);
+  return rv_host::check_launch();
+}
+
 int rv_adamw_step(int count, float* const* params, const float* const* grads,
                   float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
                   double lr, double beta1, double beta2, double eps, double weight_decay,
                   const float* step, const float* found_inf, const float* inv_scale,
                   void* stream) {
+  return rv_adamw_step_clipped(count, params, grads, exp_avg, exp_avg_sq, numel, lr, beta1, beta2,
+                               eps, weight_decay, step, found_inf, inv_scale, nullptr, stream);
+}
+
+int rv_adamw_step_clipped(int count, float* const* params, const float* const* grads,
+                          float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
+                          double lr, double beta1, double beta2, double eps, double weight_decay,
+                          const float* step, const float* found_inf, const float* inv_scale,
+                          const float* clip_coef, void* stream) {
   if (count <= 0) return count == 0 ? RV_OK : RV_ERR_BAD_SIZE;
   if (count > kMaxTensors) return RV_ERR_UNSUPPORTED;
   if (!params || !grads || !exp_avg || !exp_avg_sq || !numel || !step) return RV_ERR_NULL_POINTER;
@@ -169,6 +330,7 @@ int rv_adamw_step(int count, float* const* params, const float* const* grads,
   h.step = step;
   h.found_inf = found_inf;
   h.inv_scale = inv_scale;
+  h.clip = clip_coef;
   hipLaunchKernelGGL(adamw_k, dim3((unsigned)chunks), dim3(kThreads), 0, (hipStream_t)stream, tab,
                      h);
   return rv_host::check_launch();

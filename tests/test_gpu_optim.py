@@ -144,3 +144,71 @@ def test_many_tensors_and_rejects(cuda_device):
         FusedAdamW([q]).step()
     with pytest.raises(ValueError):
         FusedAdamW(a, amsgrad=True)
+
+
+@pytest.mark.parametrize("max_norm,shapes", [(1.0, SHAPES), (1e9, SHAPES),
+                                             (0.5, [(17 * (i + 1),) for i in range(60)])])
+def test_unscale_clip_matches_reference_sequence(cuda_device, max_norm, shapes):
+    """opt.unscale_clip_(scaler, max_norm) + scaler.step/update equals the
+    reference's scaler.unscale_ + clip_grad_norm_ + step/update (on FusedAdamW
+    both): the total norm within fp32 summation-order error, parameters within
+    a few ulps (the clip coefficient may differ in its last bit), bit for bit
+    when the clip is inactive (coefficient 1); an overflowing step is skipped
+    by both (parameters, step count) and lowers both scales alike; more
+    tensors than one launch takes (60 > 48)."""
+    base = _params(cuda_device, shapes)
+    a = [p.clone().requires_grad_(True) for p in base]
+    b = [p.clone().requires_grad_(True) for p in base]
+    opt_a = FusedAdamW(a, lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    opt_b = FusedAdamW(b, lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    sc_a, sc_b = (torch.amp.GradScaler("cuda", init_scale=2.0 ** 10) for _ in range(2))
+    one = torch.ones((), device=cuda_device)
+    for step in range(4):
+        sc_a.scale(one), sc_b.scale(one)
+        grads = [g * 100 * 2.0 ** 10 for g in _grads(base, 20 + step)]
+        if step == 2:
+            grads[1].view(-1)[0] = float("nan")
+        for params, g_ in ((a, grads), (b, grads)):
+            for p, g in zip(params, g_):
+                p.grad = g.clone()
+        sc_a.unscale_(opt_a)
+        norm_a = torch.nn.utils.clip_grad_norm_(a, max_norm)
+        sc_a.step(opt_a)
+        sc_a.update()
+        norm_b = opt_b.unscale_clip_(sc_b, max_norm)
+        sc_b.step(opt_b)
+        sc_b.update()
+        torch.cuda.synchronize()
+        if step != 2:
+            assert abs(float(norm_b) - float(norm_a)) <= 1e-5 * float(norm_a), step
+        for pa, pb in zip(a, b):
+            if max_norm >= 1e9:
+                assert torch.equal(pb, pa), step
+            else:
+                assert _close(pb.detach(), pa.detach(), rtol=2e-6, ulps=8), step
+        assert sc_a.get_scale() == sc_b.get_scale()
+    assert float(opt_b.state[b[0]]["step"]) == float(opt_a.state[a[0]]["step"]) == 3.0
+
+
+def test_clip_without_scaler(cuda_device):
+    base = _params(cuda_device, SHAPES[:4])
+    a = [p.clone().requires_grad_(True) for p in base]
+    b = [p.clone().requires_grad_(True) for p in base]
+    opt_a = FusedAdamW(a, lr=1e-3)
+    opt_b = FusedAdamW(b, lr=1e-3)
+    for pa, pb, g in zip(a, b, _grads(base, 5)):
+        pa.grad, pb.grad = g * 50, g * 50
+    norm_a = torch.nn.utils.clip_grad_norm_(a, 1.0)
+    opt_a.step()
+    norm_b = opt_b.unscale_clip_(None, 1.0)
+    opt_b.step()
+    assert abs(float(norm_b) - float(norm_a)) <= 1e-5 * float(norm_a)
+    for pa, pb in zip(a, b):
+        assert _close(pb.detach(), pa.detach(), rtol=2e-6, ulps=8)
+    with pytest.raises(RuntimeError, match="already been called"):
+        sc = torch.amp.GradScaler("cuda")
+        sc.scale(torch.ones((), device=cuda_device))
+        for p in b:
+            p.grad = torch.zeros_like(p)
+        opt_b.unscale_clip_(sc, 1.0)
+        opt_b.unscale_clip_(sc, 1.0)
