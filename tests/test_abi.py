@@ -147,3 +147,20 @@ def test_multi_cast_validates_without_device():
     assert lib.rv_cast_f32_f16_multi(n + 1, P(fake, fake), P(fake, fake), numel, None) == 3
     bad = (ctypes.c_int64 * 2)(8, -1)
     assert lib.rv_cast_f32_f16_multi(2, P(fake, fake), P(fake, fake), bad, None) == 2
+
+
+def test_grad_clip_entry_points_validate_without_device():
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)
+    n = (ctypes.c_int64 * 3)(65536, 65537, 1)
+    assert lib.rv_grad_chunks(n, 3) == 1 + 2 + 1
+    assert lib.rv_grad_chunks(n, 0) == 0
+    assert lib.rv_grad_chunks(n, -1) < 0
+    P = ctypes.c_void_p * 3
+    assert lib.rv_grad_sq_partials(0, None, None, None, None, None, 0, None) == 0
+    assert lib.rv_grad_sq_partials(3, P(fake, fake, None), n, None, fake, fake, 0, None) == 1
+    assert lib.rv_grad_sq_partials(3, P(fake, fake, fake), n, None, fake, fake, -1, None) == 2
+    assert lib.rv_grad_sq_partials(lib.rv_adamw_max_tensors() + 1, P(fake, fake, fake), n, None,
+                                   fake, fake, 0, None) == 3
+    assert lib.rv_grad_clip_coef(fake, fake, 0, 1.0, fake, fake, fake, None) == 2
+    assert lib.rv_grad_clip_coef(fake, None, 4, 1.0, fake, fake, fake, None) == 1
