@@ -159,6 +159,25 @@ int rv_rmsnorm_bwd_f16(const float* x, const float* w, const void* dy,
                        int64_t workspace_bytes, int64_t rows, int64_t width,
                        void* stream);
 
+/* The fused residual add + RMSNorm with the fp16 output: h = x + f (fp32),
+ * y = fp16(norm(h)), rstd; the midpoint force's x + A(x) and the Euler step's
+ * q + A(p) feeding M's norm (src/reversibility/reversible.py:16-25).  f fp32
+ * (RV_F32) or fp16 (RV_F16); vector path only (width % 4 == 0, aligned). */
+int rv_add_rmsnorm_fwd_f16(const float* x, const void* f, int force_dtype, const float* w,
+                           float* h, void* y, float* rstd, int64_t rows, int64_t width,
+                           float eps, void* stream);
+
+/* rv_rmsnorm_bwd with dy fp32 (RV_F32) or fp16 (RV_F16), plus: dx += dh when
+ * dh is given (the gradient of the normalized input's other uses, added as
+ * autograd's accumulation would), and dx16 = fp16(dx) when dx16 is given
+ * (the gradient of an fp16 force term of the add).  Same workspace as
+ * rv_rmsnorm_bwd; with dh or dx16 only the vector path (else
+ * RV_ERR_UNSUPPORTED). */
+int rv_rmsnorm_bwd_acc(const float* x, const float* w, const void* dy, int dy_dtype,
+                       const float* rstd, const float* dh, float* dx, void* dx16, float* dw,
+                       void* workspace, int64_t workspace_bytes, int64_t rows, int64_t width,
+                       void* stream);
+
 /* Fused residual add + RMSNorm (the x + A(x) -> mlp_norm step of
  * midpoint_force and the q' = q + A(p) -> mlp_norm step of Euler):
  *   h[r, :] = x[r, :] + S(f[r, :])             (written to h)

@@ -19,6 +19,7 @@ more than several of these kernels take on an MI355X.
 from __future__ import annotations
 
 import ctypes
+from typing import Optional
 from pathlib import Path
 
 import torch
@@ -69,6 +70,8 @@ SIGNATURES = {
     "rv_ce_bwd": (_I, [_P, _I, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P]),
     "rv_gemm_num_shapes": (_I, []),
     "rv_gemm_force_shape": (_I, [_I]),
+    "rv_add_rmsnorm_fwd_f16": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
+    "rv_rmsnorm_bwd_acc": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rv_ce_fused": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "rv_mlp_up_swiglu": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "rv_mlp_down": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
@@ -232,6 +235,43 @@ def _add_rmsnorm_fwd(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: flo
     return h, y, rstd
 
 
+def _add_rmsnorm_fwd16(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: float):
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    h = torch.empty_like(x)
+    y = torch.empty_like(x, dtype=torch.float16)
+    rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+    if rows:
+        with _DeviceGuard(x):
+            _check(library().rv_add_rmsnorm_fwd_f16(x.data_ptr(), f.data_ptr(), _dtype_code(f),
+                                                    w.data_ptr(), h.data_ptr(), y.data_ptr(),
+                                                    rstd.data_ptr(), rows, width, eps,
+                                                    _stream(x)),
+                   "rv_add_rmsnorm_fwd_f16")
+    return h, y, rstd
+
+
+def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.Tensor,
+                     dh: Optional[torch.Tensor]):
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    dx = torch.empty_like(x)
+    dx16 = torch.empty_like(x, dtype=torch.float16)
+    if not rows:
+        return dx, dx16, torch.zeros_like(w)
+    dw = torch.empty_like(w)
+    nbytes = rmsnorm_workspace_bytes(rows, width)
+    ws = torch.empty(nbytes // 4, device=x.device, dtype=torch.float32)
+    with _DeviceGuard(x):
+        _check(library().rv_rmsnorm_bwd_acc(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
+                                            _dtype_code(dy), rstd.data_ptr(),
+                                            dh.data_ptr() if dh is not None else None,
+                                            dx.data_ptr(), dx16.data_ptr(), dw.data_ptr(),
+                                            ws.data_ptr(), nbytes, rows, width, _stream(x)),
+               "rv_rmsnorm_bwd_acc")
+    return dx, dx16, dw
+
+
 def _swiglu_fwd(u: torch.Tensor):
     packed = u.shape[-1]
     width = packed // 2
@@ -333,6 +373,10 @@ _SCHEMAS = {
                     _rmsnorm_bwd),
     "add_rmsnorm_fwd": ("add_rmsnorm_fwd(Tensor x, Tensor f, Tensor weight, float eps) -> (Tensor, Tensor, Tensor)",
                         _add_rmsnorm_fwd),
+    "add_rmsnorm_fwd16": ("add_rmsnorm_fwd16(Tensor x, Tensor f, Tensor weight, float eps) "
+                          "-> (Tensor, Tensor, Tensor)", _add_rmsnorm_fwd16),
+    "rmsnorm_bwd_acc": ("rmsnorm_bwd_acc(Tensor x, Tensor weight, Tensor dy, Tensor rstd, "
+                        "Tensor? dh) -> (Tensor, Tensor, Tensor)", _rmsnorm_bwd_acc),
     "swiglu_fwd": ("swiglu_fwd(Tensor u) -> Tensor", _swiglu_fwd),
     "swiglu_bwd": ("swiglu_bwd(Tensor u, Tensor dy) -> Tensor", _swiglu_bwd),
     "midpoint_update": ("midpoint_update(Tensor p, Tensor a, Tensor m, float scale, int sign) -> Tensor",
@@ -369,6 +413,17 @@ def _(x, weight, dy, rstd):
 @torch.library.register_fake(f"{NAMESPACE}::add_rmsnorm_fwd")
 def _(x, f, weight, eps):
     return torch.empty_like(x), torch.empty_like(x), x.new_empty(_fake_rows(x), dtype=torch.float32)
+
+
+@torch.library.register_fake(f"{NAMESPACE}::add_rmsnorm_fwd16")
+def _(x, f, weight, eps):
+    return (torch.empty_like(x), torch.empty_like(x, dtype=torch.float16),
+            x.new_empty(_fake_rows(x), dtype=torch.float32))
+
+
+@torch.library.register_fake(f"{NAMESPACE}::rmsnorm_bwd_acc")
+def _(x, weight, dy, rstd, dh):
+    return torch.empty_like(x), torch.empty_like(x, dtype=torch.float16), torch.empty_like(weight)
 
 
 @torch.library.register_fake(f"{NAMESPACE}::swiglu_fwd")

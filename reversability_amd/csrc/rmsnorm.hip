@@ -57,6 +57,12 @@ constexpr int kBwdWaves = RV_RMS_BWD_WAVES;  // waves per block, backward (width
 // Waves per backward block by vector count per lane (width <= 256 * VEC):
 // 2 rows x (x, dy) x VEC float4 per register tile, two tiles in flight.
 constexpr int bwd_waves(int vec) { return vec <= 2 ? kBwdWaves : (vec == 4 ? 8 : 4); }
+// With dh accumulated the tiles are 1.5x larger: fewer waves, more registers
+// each (no scratch at width 1024).  dweight's per-row terms are then summed in
+// another fixed order (rows are dealt to waves by index) -- dx is unaffected.
+constexpr int bwd_waves(int vec, bool acc) {
+  return !acc ? bwd_waves(vec) : (vec <= 1 ? kBwdWaves : (vec == 2 ? 8 : 4));
+}
 constexpr int kMaxVec = 16;      // float4 per lane => width <= 4096
 constexpr int kMaxEpl = 64;      // scalar path: elements per lane <= 64
 
@@ -235,16 +241,20 @@ void rms_fwd_scalar(const float* __restrict__ x, const F* __restrict__ f,
 // before the current pair is reduced).  Writes dx and the block's dw partial
 // as one contiguous row, partial[block * width + col].
 // ---------------------------------------------------------------------------
-template <int VEC>
+// ACC: the row gradient also receives dh (the gradient of the normalized
+// input's other use: dx = dh + norm backward, the sum autograd would form).
+template <int VEC, bool ACC>
 struct BwdTile {
   float4 x[2][VEC], g[2][VEC];
+  float4 h[ACC ? 2 : 1][ACC ? VEC : 1];
   float rs[2];
 };
 
-template <int VEC, typename G>
-__device__ __forceinline__ void bwd_load(BwdTile<VEC>& t, const float* __restrict__ x,
+template <int VEC, bool ACC, typename G>
+__device__ __forceinline__ void bwd_load(BwdTile<VEC, ACC>& t, const float* __restrict__ x,
                                          const G* __restrict__ dy,
-                                         const float* __restrict__ rstd, int64_t row0,
+                                         const float* __restrict__ rstd,
+                                         const float* __restrict__ dh, int64_t row0,
                                          int64_t end, int width, int lane) {
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -256,13 +266,15 @@ __device__ __forceinline__ void bwd_load(BwdTile<VEC>& t, const float* __restric
       const int col_c = col < width ? col : width - 4;
       t.x[r][v] = rv::ld_f4(x + row * width + col_c);
       t.g[r][v] = rv::load4f(dy + row * width + col_c);
+      if constexpr (ACC) t.h[r][v] = rv::ld_f4(dh + row * width + col_c);
     }
   }
 }
 
-template <int VEC>
-__device__ __forceinline__ void bwd_finish(BwdTile<VEC>& t, const float4 (&wv)[VEC],
+template <int VEC, bool ACC, bool H16>
+__device__ __forceinline__ void bwd_finish(BwdTile<VEC, ACC>& t, const float4 (&wv)[VEC],
                                            float4 (&acc)[VEC], float* __restrict__ dx,
+                                           __half* __restrict__ dx16,
                                            int64_t row0, int64_t end, int width, int lane) {
   const float fwidth = (float)width;
 #pragma unroll
@@ -303,7 +315,14 @@ __device__ __forceinline__ void bwd_finish(BwdTile<VEC>& t, const float4 (&wv)[V
         o.y = (g[v].y - q.y * c) * rs;
         o.z = (g[v].z - q.z * c) * rs;
         o.w = (g[v].w - q.w * c) * rs;
+        if constexpr (ACC) {
+          o.x = o.x + t.h[r][v].x;
+          o.y = o.y + t.h[r][v].y;
+          o.z = o.z + t.h[r][v].z;
+          o.w = o.w + t.h[r][v].w;
+        }
         rv::st_f4s(dx + row * width + col, o);
+        if constexpr (H16) store_y(dx16 + row * width + col, o);
       }
     }
   }
@@ -311,12 +330,13 @@ __device__ __forceinline__ void bwd_finish(BwdTile<VEC>& t, const float4 (&wv)[V
 
 // WAVES per block: wide rows keep fewer waves so that their two-row
 // ping-pong tiles stay in registers (no scratch).
-template <int VEC, int WAVES, typename G>
+template <int VEC, int WAVES, typename G, bool ACC = false, bool H16 = false>
 __global__ __launch_bounds__(WAVES * 64)
 void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
                  const G* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
-                 int64_t rows, int width, int64_t rows_per_block) {
+                 int64_t rows, int width, int64_t rows_per_block,
+                 const float* __restrict__ dh = nullptr, __half* __restrict__ dx16 = nullptr) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t start = (int64_t)blockIdx.x * rows_per_block;
@@ -336,15 +356,15 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
   if (first < end) {  // wave-uniform
     const int64_t iters = (end - 1 - first) / stride + 1;
     int64_t row0 = first;
-    BwdTile<VEC> a, b;
-    bwd_load(a, x, dy, rstd, row0, end, width, lane);
+    BwdTile<VEC, ACC> a, b;
+    bwd_load(a, x, dy, rstd, dh, row0, end, width, lane);
     for (int64_t k = 0; k < iters; k += 2) {
-      bwd_load(b, x, dy, rstd, row0 + stride, end, width, lane);
-      bwd_finish(a, wv, acc, dx, row0, end, width, lane);
+      bwd_load(b, x, dy, rstd, dh, row0 + stride, end, width, lane);
+      bwd_finish<VEC, ACC, H16>(a, wv, acc, dx, dx16, row0, end, width, lane);
       if (k + 1 >= iters) break;
       row0 += stride;
-      bwd_load(a, x, dy, rstd, row0 + stride, end, width, lane);
-      bwd_finish(b, wv, acc, dx, row0, end, width, lane);
+      bwd_load(a, x, dy, rstd, dh, row0 + stride, end, width, lane);
+      bwd_finish<VEC, ACC, H16>(b, wv, acc, dx, dx16, row0, end, width, lane);
       row0 += stride;
     }
   }
@@ -544,7 +564,8 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, Y* y,
 template <typename G>
 int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, float* dx,
                float* dw, void* workspace, int64_t workspace_bytes, int64_t rows,
-               int64_t width, hipStream_t s) {
+               int64_t width, hipStream_t s, const float* dh = nullptr,
+               __half* dx16 = nullptr) {
   if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > 4096) return RV_ERR_UNSUPPORTED;
@@ -559,18 +580,29 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
   const bool vec = (width % 4 == 0) && rv_host::aligned16(x) &&
                    rv_host::aligned16(w) &&
                    (reinterpret_cast<uintptr_t>(dy) % (4 * sizeof(G))) == 0 &&
-                   rv_host::aligned16(dx);
+                   rv_host::aligned16(dx) && (dh == nullptr || rv_host::aligned16(dh)) &&
+                   (reinterpret_cast<uintptr_t>(dx16) % 8) == 0;
+  if (!vec && (dh != nullptr || dx16 != nullptr)) return RV_ERR_UNSUPPORTED;
   if (vec) {
     const int vecs = (iw + 255) / 256;
-#define RV_BWD_VEC(V)                                                             \
-  hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V), G>), grid, dim3(bwd_waves(V) * 64), 0, s, x, \
-                     w, dy, rstd, dx, partial, rows, iw, p.rows_per_block)
+#define RV_BWD_VEC_K(V, ACC, H16)                                                         \
+  hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V, ACC), G, ACC, H16>), grid,              \
+                     dim3(bwd_waves(V, ACC) * 64), 0, s, x, w, dy, rstd, dx, partial, rows,  \
+                     iw, p.rows_per_block, dh, dx16)
+#define RV_BWD_VEC(V)                                                \
+  do {                                                               \
+    if (dh != nullptr && dx16 != nullptr) RV_BWD_VEC_K(V, true, true);   \
+    else if (dh != nullptr) RV_BWD_VEC_K(V, true, false);            \
+    else if (dx16 != nullptr) RV_BWD_VEC_K(V, false, true);          \
+    else RV_BWD_VEC_K(V, false, false);                              \
+  } while (0)
     if (vecs <= 1) RV_BWD_VEC(1);
     else if (vecs <= 2) RV_BWD_VEC(2);
     else if (vecs <= 4) RV_BWD_VEC(4);
     else if (vecs <= 8) RV_BWD_VEC(8);
     else RV_BWD_VEC(16);
 #undef RV_BWD_VEC
+#undef RV_BWD_VEC_K
   } else if constexpr (!std::is_same<G, float>::value) {
     return RV_ERR_UNSUPPORTED;  // fp16 gradient: vector path only
   } else {
@@ -658,6 +690,44 @@ int rv_rmsnorm_bwd_f16(const float* x, const float* w, const void* dy, const flo
                        int64_t rows, int64_t width, void* stream) {
   return launch_bwd<__half>(x, w, static_cast<const __half*>(dy), rstd, dx, dw, workspace,
                             workspace_bytes, rows, width, (hipStream_t)stream);
+}
+
+int rv_add_rmsnorm_fwd_f16(const float* x, const void* f, int force_dtype, const float* w,
+                           float* h, void* y, float* rstd, int64_t rows, int64_t width,
+                           float eps, void* stream) {
+  if (!x || !f || !w || !h || !y || !rstd) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096) return RV_ERR_UNSUPPORTED;
+  const hipStream_t s = (hipStream_t)stream;
+  __half* y16 = static_cast<__half*>(y);
+  switch (force_dtype) {
+    case RV_F32:
+      return launch_fwd<float, true, __half>(x, (const float*)f, w, h, y16, rstd, rows,
+                                             (int)width, eps, s);
+    case RV_F16:
+      return launch_fwd<__half, true, __half>(x, (const __half*)f, w, h, y16, rstd, rows,
+                                              (int)width, eps, s);
+    default:
+      return RV_ERR_UNSUPPORTED;
+  }
+}
+
+int rv_rmsnorm_bwd_acc(const float* x, const float* w, const void* dy, int dy_dtype,
+                       const float* rstd, const float* dh, float* dx, void* dx16, float* dw,
+                       void* workspace, int64_t workspace_bytes, int64_t rows, int64_t width,
+                       void* stream) {
+  const hipStream_t s = (hipStream_t)stream;
+  __half* d16 = static_cast<__half*>(dx16);
+  switch (dy_dtype) {
+    case RV_F32:
+      return launch_bwd<float>(x, w, static_cast<const float*>(dy), rstd, dx, dw, workspace,
+                               workspace_bytes, rows, width, s, dh, d16);
+    case RV_F16:
+      return launch_bwd<__half>(x, w, static_cast<const __half*>(dy), rstd, dx, dw, workspace,
+                                workspace_bytes, rows, width, s, dh, d16);
+    default:
+      return RV_ERR_UNSUPPORTED;
+  }
 }
 
 }  // extern "C"

@@ -62,6 +62,54 @@ class FusedRMSNorm(torch.autograd.Function):
         return dx, dweight, None, None
 
 
+class FusedAddRMSNorm(torch.autograd.Function):
+    """``(h, y) = (x + f, RMSNorm(x + f))`` for the fp32 residual stream x and
+    a force term f (fp16 or fp32), y as FusedRMSNorm's fp16 output: the
+    residual add that feeds a norm (the midpoint force's ``x + A(x)``, the
+    Euler step's ``q + A(p)``; src/reversibility/reversible.py:16-25) in the
+    norm's own pass (``rv_add_rmsnorm_fwd_f16``).  Backward in one pass too
+    (``rv_rmsnorm_bwd_acc``): the input gradient is the norm backward plus
+    the gradient of h's other uses -- the sum autograd would form -- written
+    in fp32 for x and rounded to fp16 for f.  Same values as the add, the
+    norm and autograd's accumulation and cast."""
+
+    @staticmethod
+    def forward(ctx, x, f, weight, eps):
+        ctx.set_materialize_grads(False)
+        h, y, rstd = ops.add_rmsnorm_fwd16(x, f, weight.contiguous(), float(eps))
+        ctx.save_for_backward(h, weight, rstd)
+        ctx.f_dtype = f.dtype
+        return h, y
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dh, dy):
+        h, weight, rstd = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(h, dtype=torch.float16)
+        elif dy.dtype not in (torch.float32, torch.float16):
+            dy = dy.float()
+        dx, dx16, dweight = ops.rmsnorm_bwd_acc(h, weight.contiguous(), dy.contiguous(), rstd,
+                                                dh.contiguous() if dh is not None else None)
+        df = dx16 if ctx.f_dtype == torch.float16 else dx.to(ctx.f_dtype)
+        return dx, df, dweight, None
+
+
+def add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
+    """``(h, norm(h))`` with ``h = x + f``.  On the fused kernels when ``norm``
+    is an RMSNorm routed by ``enable_rmsnorm(..., fp16_out=True)`` and the
+    call runs under fp16 autocast on the GPU; otherwise the residual add
+    (``residual.euler_step``) followed by ``norm``."""
+    if (getattr(norm, "_rv_fp16_out", False) and x.is_cuda and x.dtype == torch.float32
+            and f.dtype in (torch.float16, torch.float32) and x.shape == f.shape
+            and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
+            and _fp16_out(x)):
+        return FusedAddRMSNorm.apply(x, f, norm.weight, rms_norm_eps(norm, x))
+    from .residual import euler_step
+    h = euler_step(x, f, +1)
+    return h, norm(h)
+
+
 def rms_norm_eps(module: torch.nn.RMSNorm, x: torch.Tensor) -> float:
     """The eps nn.RMSNorm uses: its own, else finfo(x.dtype).eps (kernels_v3.py:79)."""
     return module.eps if module.eps is not None else torch.finfo(x.dtype).eps
@@ -77,3 +125,4 @@ def enable_rmsnorm(model: torch.nn.Module, fp16_out: bool = False) -> None:
         if isinstance(module, torch.nn.RMSNorm):
             module.forward = types.MethodType(forward, module)
             module._rv_fused = True
+            module._rv_fp16_out = bool(fp16_out)

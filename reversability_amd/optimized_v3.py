@@ -25,6 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
+from .kernels_v3 import add_rms_norm
 from .optimized import ReusedMidpoint, amp_context, hidden_states
 from .residual import midpoint_step
 
@@ -235,7 +236,7 @@ class SplitMidpoint(torch.autograd.Function):
                 with torch.enable_grad():
                     previous_q = p.detach().requires_grad_(True)
                     proxy = attention.detach().requires_grad_(True)
-                    mlp = block.mlp(block.mlp_norm(previous_q + proxy))
+                    mlp = block.mlp(add_rms_norm(previous_q, proxy, block.mlp_norm)[1])
                     with torch.no_grad():
                         previous_p = midpoint_step(q, proxy.detach(), mlp.detach(), scale, -1)
                     previous_p.requires_grad_(True)

@@ -24,14 +24,16 @@ import math
 import torch
 from torch.autograd.function import once_differentiable
 
+from .kernels_v3 import add_rms_norm
 from .model import BaselineLM, Block, ModelConfig
 from .residual import euler_step, midpoint_step
 
 
 def midpoint_terms(block: Block, x: torch.Tensor):
-    """(A(x), M(x + A(x))) -- the two summands of the midpoint force."""
+    """(A(x), M(x + A(x))) -- the two summands of the midpoint force (the add
+    and M's norm in one pass where the fused norm applies)."""
     attention = block.attn(block.attn_norm(x))
-    return attention, block.mlp(block.mlp_norm(x + attention))
+    return attention, block.mlp(add_rms_norm(x, attention, block.mlp_norm)[1])
 
 
 def midpoint_force(block: Block, x: torch.Tensor) -> torch.Tensor:
@@ -45,8 +47,8 @@ def forward_pair(block, p, q, method, h):
     if method == "midpoint":
         attention, mlp = midpoint_terms(block, q)
         return q, midpoint_step(p, attention, mlp, 2 * h, +1)
-    next_q = euler_step(q, block.attn(block.attn_norm(p)), +1)
-    return euler_step(p, block.mlp(block.mlp_norm(next_q)), +1), next_q
+    next_q, normed = add_rms_norm(q, block.attn(block.attn_norm(p)), block.mlp_norm)
+    return euler_step(p, block.mlp(normed), +1), next_q
 
 
 def inverse_pair(block, p, q, method, h):
@@ -77,8 +79,8 @@ def _euler_inverse_for_vjp(block, p, q):
         with torch.no_grad():
             q0 = euler_step(q, attention.detach(), -1)
         q0 = q0.detach().requires_grad_(True)
-        next_q = euler_step(q0, attention, +1)
-        next_p = euler_step(p0, block.mlp(block.mlp_norm(next_q)), +1)
+        next_q, normed = add_rms_norm(q0, attention, block.mlp_norm)
+        next_p = euler_step(p0, block.mlp(normed), +1)
     return next_p, next_q, p0, q0
 
 

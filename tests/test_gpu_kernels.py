@@ -289,3 +289,45 @@ def test_residual_axpy_bitwise(cuda_device, sign):
     f = torch.randn(16896 * 256 + 1, generator=g).half()
     out = ops.residual_axpy(x.to(cuda_device), f.to(cuda_device), sign).cpu()
     assert np.array_equal(out.numpy(), oracle.euler(x.numpy(), f.numpy(), sign))
+
+
+@pytest.mark.parametrize("rows,width,f_dtype,use_h", [(1000, 256, torch.float16, True),
+                                                      (777, 1024, torch.float16, False),
+                                                      (777, 1024, torch.float16, True),
+                                                      (64, 256, torch.float32, True)])
+def test_fused_add_rmsnorm_matches_composition_bitwise(cuda_device, rows, width, f_dtype, use_h):
+    """FusedAddRMSNorm = residual add (euler_step) + FusedRMSNorm(fp16 out) +
+    autograd's accumulation of h's gradients and the fp16 cast of f's, bit for
+    bit: h, y, dx, df, with and without another use of h.  dweight too, except
+    where the accumulating backward runs fewer waves per block (width > 256
+    with another use of h: 4 instead of 8 at width 1024, to keep its larger
+    register tiles unspilled), which sums the same per-row terms in another
+    fixed order: there within fp32 summation error."""
+    from reversability_amd.kernels_v3 import FusedAddRMSNorm
+    from reversability_amd.residual import euler_step
+    g = torch.Generator().manual_seed(rows + width)
+    x0 = torch.randn(rows, width, generator=g).to(cuda_device)
+    f0 = torch.randn(rows, width, generator=g).to(f_dtype).to(cuda_device)
+    w0 = (1 + 0.02 * torch.randn(width, generator=g)).to(cuda_device)
+    gy = torch.randn(rows, width, generator=g).half().to(cuda_device)
+    gh = torch.randn(rows, width, generator=g).to(cuda_device)
+    eps = float(torch.finfo(torch.float32).eps)
+    outs = []
+    for fused in (True, False):
+        x, f, w = (t.clone().requires_grad_(True) for t in (x0, f0, w0))
+        with torch.autocast("cuda", dtype=torch.float16):
+            if fused:
+                h, y = FusedAddRMSNorm.apply(x, f, w, eps)
+            else:
+                h = euler_step(x, f, +1)
+                y = FusedRMSNorm.apply(h, w, eps, True)
+        assert y.dtype == torch.float16
+        loss = (y.float() * gy.float()).sum() + ((h * gh).sum() if use_h else 0)
+        loss.backward()
+        outs.append((h.detach(), y.detach(), x.grad, f.grad, w.grad))
+    for i, (a, b) in enumerate(zip(*outs)):
+        assert a.dtype == b.dtype
+        if i == 4 and use_h and width > 256:
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-6)
+        else:
+            assert torch.equal(a, b), i
