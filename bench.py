@@ -33,8 +33,10 @@ Also reported, on the same line:
   train_step    configs[3]: midpoint-reversible 7-layer decoder step
                 (B=33, T=512, fp16 autocast, GradScaler, clip 1.0, AdamW)
                 on the reference's v3 probe path (install_v3 split core,
-                8192-token MLP tiles, fused SwiGLU + RMSNorm, cached head with
-                the fused cross-entropy), in tokens/s.
+                a whole-batch MLP tile, fused SwiGLU + RMSNorm, cached head
+                with the fused cross-entropy), in tokens/s: the update
+                captured once in a HIP graph and replayed (``launch``), the
+                same update launched eagerly beside it (``eager_*``).
   train_step_c5 configs[4]: the 12-layer Hamiltonian-Euler d1024 step on
                 the same kernels (reconstruction-stack core), tokens/s.
   cpu_baseline  the CPU oracle (oracle/kernels_ref.c, OpenMP) on the host's
@@ -85,6 +87,8 @@ def parse_args():
                    help="only the kernel loop (used under rocprofv3)")
     p.add_argument("--mlp-only", action="store_true",
                    help="only the MLP block and MLP GEMM measurements (used under rocprofv3)")
+    p.add_argument("--train-only", choices=sorted(TRAIN_CONFIGS),
+                   help="only the named training step (--train-steps / --train-warmup)")
     p.add_argument("--attn-only", action="store_true",
                    help="only the attention and embedding measurements (used under rocprofv3)")
     return p.parse_args()
@@ -222,7 +226,7 @@ def kernel_loop_only(dev, steps: int, warmup: int) -> None:
 
 
 TRAIN_CONFIGS = {
-    # midpoint 7 layers, d 256, split core, 8192-token MLP tiles
+    # midpoint 7 layers, d 256, split core, whole-batch MLP tile (MLP_TOKENS)
     "c4": {"model": {"vocab_size": 50257, "max_sequence_length": 512, "n_layers": 7,
                      "n_heads": 8, "d_model": 256, "d_ff": 1024},
            "method": "midpoint", "step_size": 0.5, "batch": 33, "core_mode": "split",
@@ -252,7 +256,7 @@ def make_train_step(dev, name: str):
     """One full training update of a TRAIN_CONFIGS entry, on the reference's
     v3 probe path (scripts/benchmark_midpoint_v3.py:78-83 over
     scripts/benchmark_optimized.py:54-82): install_v3 (split core for the
-    midpoint config, 8192-token tiled MLP keeping its tiles for its backward,
+    midpoint config, tiled MLP (MLP_TOKENS) keeping its tiles for its backward,
     fused SwiGLU and RMSNorm), the
     attention projections and the causal attention itself on the MFMA kernels
     (enable_linear, enable_attention), the fused token +
@@ -262,7 +266,8 @@ def make_train_step(dev, name: str):
     cached_head_backward -- fp16 autocast core forward, the tied head and the
     fused cross-entropy in HEAD_CHUNK-token chunks, sum loss / valid targets, one
     core backward -- then GradScaler unscale, clip 1.0 and AdamW (0.9, 0.95),
-    wd 0.1 (FusedAdamW: one multi-tensor HIP pass, no host synchronisation).
+    wd 0.1 (FusedAdamW.unscale_clip_: one gradient-norm pass; the update applies
+    unscale and clip as it reads each gradient; no host synchronisation).
     Returns (step function returning the summed loss, targets per step,
     config)."""
     import numpy as np
@@ -595,6 +600,10 @@ def main() -> int:
     if args.mlp_only:
         print(json.dumps({"mlp_block": mlp_block_bench(dev), "mlp_gemms": mlp_gemm_bench(dev)}),
               flush=True)
+        return 0
+    if args.train_only:
+        print(json.dumps({f"train_step_{args.train_only}": train_step_bench(
+            dev, args.train_steps, args.train_warmup, args.train_only)}), flush=True)
         return 0
     if args.attn_only:
         print(json.dumps({"attention": attention_bench(dev), "embedding": embedding_bench(dev)}),
