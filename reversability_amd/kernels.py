@@ -66,7 +66,7 @@ FUSED_CE_MAX_COLS = 65536
 
 
 def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: torch.Tensor,
-                 grad: torch.Tensor):
+                 grad: torch.Tensor, dx_out: torch.Tensor | None = None):
     """One chunk of the tied head and its summed cross-entropy, forward and
     backward, with the logits stored at a padded row stride.
 
@@ -79,7 +79,8 @@ def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: to
     the fp16 head with its rows padded to a multiple of VOCAB_ALIGN (the pad
     rows zero), so every logits row starts 16-byte aligned: with the odd
     vocabulary (50257) as the row stride, hipBLASLt's GEMMs over the logits
-    run 15-25% slower on MI355X.  Returns (loss sum, dx16, dW16 [vocab, d]).
+    run 15-25% slower on MI355X.  Returns (loss sum, dx16, dW16 [vocab, d]);
+    dx16 is written into ``dx_out`` (contiguous fp16 [rows, d]) when given.
     """
     rows, d = x16.shape
     padded = head16.shape[0]
@@ -113,7 +114,10 @@ def tied_head_ce(x16: torch.Tensor, head16: torch.Tensor, vocab: int, labels: to
                                  IGNORE_INDEX, dlogits.data_ptr(), st), "rv_ce_bwd")
     del logits
     d_view = dlogits[:, :vocab]
-    dx16 = torch.mm(d_view, head16[:vocab])
+    if dx_out is not None:
+        dx16 = torch.mm(d_view, head16[:vocab], out=dx_out)
+    else:
+        dx16 = torch.mm(d_view, head16[:vocab])
     dw16 = torch.mm(d_view.t(), x16)
     return losses.sum(), dx16, dw16
 

@@ -286,9 +286,12 @@ def _fused_head(hidden, weight, labels, denominator, chunk_tokens, scaler, preci
     total = torch.zeros((), device=device, dtype=torch.float32)
     for start in range(0, targets.numel(), chunk_tokens):
         stop = start + chunk_tokens
+        rows = dflat[start:stop]
+        direct = rows.dtype == torch.float16 and rows.is_contiguous()
         loss, dx16, dw16 = tied_head_ce(x16[start:stop], head16, vocab, targets[start:stop],
-                                        grad.reshape(1))
-        dflat[start:stop].copy_(dx16)
+                                        grad.reshape(1), dx_out=rows if direct else None)
+        if not direct:
+            rows.copy_(dx16)
         chunk_grad = dw16.to(weight.dtype)
         if weight.grad is None:
             weight.grad = chunk_grad

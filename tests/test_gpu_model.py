@@ -401,8 +401,9 @@ def test_split_midpoint_kept_attention_bitwise(cuda_device):
         assert torch.equal(a, b)
 
 
-def test_captured_train_step_matches_eager_bitwise(cuda_device):
-    """The whole configs[3] update (bench.make_train_step: batch cut on the
+@pytest.mark.parametrize("config", ["c4", "c5"])
+def test_captured_train_step_matches_eager_bitwise(cuda_device, config):
+    """The whole configs[3] / configs[4] update (bench.make_train_step: batch cut on the
     device, fp16 core forward and reconstruction backward, tied head and fused
     cross-entropy, GradScaler unscale, clip, FusedAdamW) captured once in a
     HIP graph and replayed equals the eager update of a twin model bit for
@@ -412,8 +413,8 @@ def test_captured_train_step_matches_eager_bitwise(cuda_device):
     a no-op)."""
     import bench
     from reversability_amd.graph import CapturedStep
-    eager, _, _ = bench.make_train_step(cuda_device, "c4")
-    graphed, _, _ = bench.make_train_step(cuda_device, "c4")
+    eager, _, _ = bench.make_train_step(cuda_device, config)
+    graphed, _, _ = bench.make_train_step(cuda_device, config)
     captured = CapturedStep(graphed, warmup=3)
     for _ in range(3):  # the capture's warm-up updates
         eager()
