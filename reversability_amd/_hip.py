@@ -252,11 +252,12 @@ def _add_rmsnorm_fwd16(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: f
 
 
 def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.Tensor,
-                     dh: Optional[torch.Tensor]):
+                     dh: Optional[torch.Tensor], f16: bool = True):
     width = x.shape[-1]
     rows = x.numel() // width if width else 0
     dx = torch.empty_like(x)
-    dx16 = torch.empty_like(x, dtype=torch.float16)
+    dx16 = (torch.empty_like(x, dtype=torch.float16) if f16
+            else x.new_empty(0, dtype=torch.float16))
     if not rows:
         return dx, dx16, torch.zeros_like(w)
     dw = torch.empty_like(w)
@@ -266,7 +267,8 @@ def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: t
         _check(library().rv_rmsnorm_bwd_acc(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
                                             _dtype_code(dy), rstd.data_ptr(),
                                             dh.data_ptr() if dh is not None else None,
-                                            dx.data_ptr(), dx16.data_ptr(), dw.data_ptr(),
+                                            dx.data_ptr(), dx16.data_ptr() if f16 else None,
+                                            dw.data_ptr(),
                                             ws.data_ptr(), nbytes, rows, width, _stream(x)),
                "rv_rmsnorm_bwd_acc")
     return dx, dx16, dw
@@ -376,7 +378,8 @@ _SCHEMAS = {
     "add_rmsnorm_fwd16": ("add_rmsnorm_fwd16(Tensor x, Tensor f, Tensor weight, float eps) "
                           "-> (Tensor, Tensor, Tensor)", _add_rmsnorm_fwd16),
     "rmsnorm_bwd_acc": ("rmsnorm_bwd_acc(Tensor x, Tensor weight, Tensor dy, Tensor rstd, "
-                        "Tensor? dh) -> (Tensor, Tensor, Tensor)", _rmsnorm_bwd_acc),
+                        "Tensor? dh, bool f16=True) -> (Tensor, Tensor, Tensor)",
+                        _rmsnorm_bwd_acc),
     "swiglu_fwd": ("swiglu_fwd(Tensor u) -> Tensor", _swiglu_fwd),
     "swiglu_bwd": ("swiglu_bwd(Tensor u, Tensor dy) -> Tensor", _swiglu_bwd),
     "midpoint_update": ("midpoint_update(Tensor p, Tensor a, Tensor m, float scale, int sign) -> Tensor",
@@ -422,8 +425,9 @@ def _(x, f, weight, eps):
 
 
 @torch.library.register_fake(f"{NAMESPACE}::rmsnorm_bwd_acc")
-def _(x, weight, dy, rstd, dh):
-    return torch.empty_like(x), torch.empty_like(x, dtype=torch.float16), torch.empty_like(weight)
+def _(x, weight, dy, rstd, dh, f16=True):
+    return (torch.empty_like(x), torch.empty_like(x, dtype=torch.float16) if f16
+            else x.new_empty(0, dtype=torch.float16), torch.empty_like(weight))
 
 
 @torch.library.register_fake(f"{NAMESPACE}::swiglu_fwd")

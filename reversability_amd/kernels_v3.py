@@ -95,6 +95,49 @@ class FusedAddRMSNorm(torch.autograd.Function):
         return dx, df, dweight, None
 
 
+class FusedRMSNormPass(torch.autograd.Function):
+    """``(x, RMSNorm(x))`` -- the normalized input passed through as a second
+    output, for an x that also feeds something else (the Euler step's
+    ``p0 + M(...)`` beside ``attn_norm(p0)``; the split midpoint's MLP graph
+    beside the attention graph).  Backward in one pass: the norm backward plus
+    the pass-through output's gradient (``rv_rmsnorm_bwd_acc``), the sum
+    autograd would otherwise form in a separate kernel.  y as FusedRMSNorm's
+    (fp16 under fp16 autocast with ``fp16_out``)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, fp16_out=False):
+        ctx.set_materialize_grads(False)
+        half = bool(fp16_out) and _fp16_out(x)
+        y, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps), half)
+        ctx.save_for_backward(x, weight, rstd)
+        return x.view_as(x), y
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dpass, dy):
+        x, weight, rstd = ctx.saved_tensors
+        if dy is None:
+            return dpass, None, None, None
+        if dy.dtype not in (torch.float32, torch.float16):
+            dy = dy.float()
+        dx, _, dweight = ops.rmsnorm_bwd_acc(x, weight.contiguous(), dy.contiguous(), rstd,
+                                             dpass.contiguous() if dpass is not None else None,
+                                             False)
+        return dx, dweight, None, None
+
+
+def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module):
+    """``(x', norm(x))`` with x' = x for x's other use (see FusedRMSNormPass), on the
+    fused kernels when ``norm`` is routed by ``enable_rmsnorm`` and x is a
+    contiguous fp32 GPU tensor whose rows the vector kernels cover; otherwise
+    ``(x, norm(x))``."""
+    if (getattr(norm, "_rv_fused", False) and x.is_cuda and x.dtype == torch.float32
+            and x.is_contiguous() and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0):
+        return FusedRMSNormPass.apply(x, norm.weight, rms_norm_eps(norm, x),
+                                      getattr(norm, "_rv_fp16_out", False))
+    return x, norm(x)
+
+
 def add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
     """``(h, norm(h))`` with ``h = x + f``.  On the fused kernels when ``norm``
     is an RMSNorm routed by ``enable_rmsnorm(..., fp16_out=True)`` and the

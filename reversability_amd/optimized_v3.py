@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
-from .kernels_v3 import add_rms_norm
+from .kernels_v3 import add_rms_norm, rms_norm_pass
 from .optimized import ReusedMidpoint, amp_context, hidden_states
 from .residual import midpoint_step
 
@@ -229,7 +229,8 @@ class SplitMidpoint(torch.autograd.Function):
                 if KEEP_SPLIT_ATTENTION:  # its graph serves the attention VJP below
                     with torch.enable_grad():
                         attn_input = p.detach().requires_grad_(True)
-                        attention = block.attn(block.attn_norm(attn_input))
+                        attn_pass, normed = rms_norm_pass(attn_input, block.attn_norm)
+                        attention = block.attn(normed)
                 else:
                     with torch.no_grad():
                         attention = block.attn(block.attn_norm(p))
@@ -251,16 +252,21 @@ class SplitMidpoint(torch.autograd.Function):
                 with torch.enable_grad():
                     if not KEEP_SPLIT_ATTENTION:
                         attn_input = previous_q.detach().requires_grad_(True)
-                        attention = block.attn(block.attn_norm(attn_input))
+                        attn_pass, normed = rms_norm_pass(attn_input, block.attn_norm)
+                        attention = block.attn(normed)
                     attention_parameters = (*block.attn_norm.parameters(), *block.attn.parameters())
-                    attn_local = torch.autograd.grad(attention, (attn_input, *attention_parameters),
-                                                     attention_cotangent)
-                dp, dq = next_dp, q_mlp + attn_local[0]
+                    # q's two gradients (MLP graph, attention graph) are summed in
+                    # the attention norm's backward pass: q_mlp enters as the
+                    # gradient of the norm's pass-through output
+                    attn_local = torch.autograd.grad((attention, attn_pass),
+                                                     (attn_input, *attention_parameters),
+                                                     (attention_cotangent, q_mlp))
+                dp, dq = next_dp, attn_local[0]
                 by_id = {id(w): g for w, g in zip((*attention_parameters, *mlp_parameters),
                                                   (*attn_local[1:], *mlp_grads))}
                 grads[0:0] = [by_id[id(w)] for w in block.parameters()]
                 p, q = previous_p.detach(), previous_q.detach()
-                del attn_input, attention, attn_local, attention_cotangent, q_mlp, by_id, mlp_grads
+                del attn_input, attn_pass, normed, attention, attn_local, attention_cotangent, q_mlp, by_id, mlp_grads
         return (dp, dq, None, None, *grads)
 
 

@@ -24,7 +24,7 @@ import math
 import torch
 from torch.autograd.function import once_differentiable
 
-from .kernels_v3 import add_rms_norm
+from .kernels_v3 import add_rms_norm, rms_norm_pass
 from .model import BaselineLM, Block, ModelConfig
 from .residual import euler_step, midpoint_step
 
@@ -75,12 +75,15 @@ def _euler_inverse_for_vjp(block, p, q):
         p0 = euler_step(p, block.mlp(block.mlp_norm(q)), -1)
     with torch.enable_grad():
         p0 = p0.detach().requires_grad_(True)
-        attention = block.attn(block.attn_norm(p0))
+        # p0 feeds attn_norm and next_p: its two gradients are summed in the
+        # norm's backward pass (rms_norm_pass)
+        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm)
+        attention = block.attn(normed_p0)
         with torch.no_grad():
             q0 = euler_step(q, attention.detach(), -1)
         q0 = q0.detach().requires_grad_(True)
         next_q, normed = add_rms_norm(q0, attention, block.mlp_norm)
-        next_p = euler_step(p0, block.mlp(normed), +1)
+        next_p = euler_step(p0_pass, block.mlp(normed), +1)
     return next_p, next_q, p0, q0
 
 

@@ -331,3 +331,36 @@ def test_fused_add_rmsnorm_matches_composition_bitwise(cuda_device, rows, width,
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-6)
         else:
             assert torch.equal(a, b), i
+
+
+@pytest.mark.parametrize("rows,width,fp16_out", [(1000, 256, True), (777, 1024, True),
+                                                 (300, 256, False)])
+def test_rmsnorm_pass_matches_composition(cuda_device, rows, width, fp16_out):
+    """FusedRMSNormPass = the norm + autograd's sum of x's two gradients (the
+    norm's and the pass-through use's): y, dx bit for bit; dweight too except
+    at width > 256 (the accumulating backward's 4 waves per block sum the
+    same per-row terms in another fixed order: within fp32 summation error)."""
+    from reversability_amd.kernels_v3 import FusedRMSNormPass
+    g = torch.Generator().manual_seed(rows * 3 + width)
+    x0 = torch.randn(rows, width, generator=g).to(cuda_device)
+    w0 = (1 + 0.02 * torch.randn(width, generator=g)).to(cuda_device)
+    gy = torch.randn(rows, width, generator=g).to(cuda_device)
+    gp = torch.randn(rows, width, generator=g).to(cuda_device)
+    eps = float(torch.finfo(torch.float32).eps)
+    outs = []
+    for fused in (True, False):
+        x, w = x0.clone().requires_grad_(True), w0.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.float16, enabled=fp16_out):
+            if fused:
+                xp, y = FusedRMSNormPass.apply(x, w, eps, fp16_out)
+            else:
+                xp, y = x, FusedRMSNorm.apply(x, w, eps, fp16_out)
+        loss = (y.float() * gy).sum() + (xp * gp).sum()
+        loss.backward()
+        outs.append((y.detach(), x.grad, w.grad))
+    (y1, dx1, dw1), (y2, dx2, dw2) = outs
+    assert torch.equal(y1, y2) and torch.equal(dx1, dx2)
+    if width > 256:
+        assert torch.allclose(dw1, dw2, rtol=1e-5, atol=1e-6)
+    else:
+        assert torch.equal(dw1, dw2)
