@@ -47,7 +47,8 @@ class ReusedMidpoint(torch.autograd.Function):
                     with torch.no_grad():
                         previous_p = midpoint_step(q, attention.detach(), mlp.detach(), scale, -1)
                     previous_p.requires_grad_(True)
-                    next_q = midpoint_step(previous_p, attention, mlp, scale, +1)
+                    # only differentiated: its value is never read
+                    next_q = midpoint_step(previous_p, attention, mlp, scale, +1, graph_only=True)
                     # (previous_q, next_q) are the layer's outputs (next_p, next_q).
                     local = torch.autograd.grad((previous_q, next_q),
                                                 (previous_p, previous_q, *block.parameters()),

@@ -241,7 +241,8 @@ class SplitMidpoint(torch.autograd.Function):
                     with torch.no_grad():
                         previous_p = midpoint_step(q, proxy.detach(), mlp.detach(), scale, -1)
                     previous_p.requires_grad_(True)
-                    next_q = midpoint_step(previous_p, proxy, mlp, scale, +1)
+                    # only differentiated: its value is never read
+                    next_q = midpoint_step(previous_p, proxy, mlp, scale, +1, graph_only=True)
                     mlp_parameters = (*block.mlp_norm.parameters(), *block.mlp.parameters())
                     local = torch.autograd.grad((previous_q, next_q),
                                                 (previous_p, previous_q, proxy, *mlp_parameters),

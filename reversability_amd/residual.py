@@ -40,12 +40,17 @@ def _state_force(p: torch.Tensor, a: torch.Tensor, m: torch.Tensor | None = None
 
 class MidpointStep(torch.autograd.Function):
     """out = p + sign * round(round(a + m) * scale); grads: dp = dout,
-    da = dm = sign * round(round(dout) * scale) (autograd through the eager form)."""
+    da = dm = sign * round(round(dout) * scale) (autograd through the eager form).
+    The backward needs no forward value: with ``graph_only`` the output is
+    allocated but not computed (for a rebuilt graph whose output value is
+    never read, only differentiated)."""
 
     @staticmethod
-    def forward(ctx, p, a, m, scale, sign):
+    def forward(ctx, p, a, m, scale, sign, graph_only=False):
         p, a, m = _state_force(p, a, m)
         ctx.scale, ctx.sign, ctx.force_dtype = float(scale), int(sign), a.dtype
+        if graph_only:
+            return torch.empty_like(p)
         return ops.midpoint_update(p, a, m, float(scale), int(sign))
 
     @staticmethod
@@ -53,35 +58,40 @@ class MidpointStep(torch.autograd.Function):
     def backward(ctx, dout):
         dout = dout.contiguous()
         da = ops.midpoint_update_bwd(dout, ctx.scale, ctx.sign, ctx.force_dtype)
-        return dout, da, da, None, None
+        return dout, da, da, None, None, None
 
 
 class EulerStep(torch.autograd.Function):
-    """out = x + sign * f; grads: dx = dout, df = sign * dout cast to f's dtype."""
+    """out = x + sign * f; grads: dx = dout, df = sign * dout cast to f's dtype.
+    ``graph_only``: as MidpointStep's."""
 
     @staticmethod
-    def forward(ctx, x, f, sign):
+    def forward(ctx, x, f, sign, graph_only=False):
         x, f, _ = _state_force(x, f)
         ctx.sign, ctx.force_dtype = int(sign), f.dtype
+        if graph_only:
+            return torch.empty_like(x)
         return ops.residual_axpy(x, f, int(sign))
 
     @staticmethod
     @once_differentiable
     def backward(ctx, dout):
         df = dout if ctx.sign > 0 else -dout
-        return dout, df.to(ctx.force_dtype), None
+        return dout, df.to(ctx.force_dtype), None, None
 
 
-def midpoint_step(p, a, m, scale, sign):
-    """p + sign * scale * (a + m) with the eager rounding points."""
+def midpoint_step(p, a, m, scale, sign, graph_only=False):
+    """p + sign * scale * (a + m) with the eager rounding points.  ``graph_only``
+    (GPU only): the caller differentiates the result but never reads it, so the
+    value is not computed (its memory is left as allocated)."""
     if p.device.type == "cuda":
-        return MidpointStep.apply(p, a, m, scale, sign)
+        return MidpointStep.apply(p, a, m, scale, sign, graph_only)
     force = a + m
     return p + scale * force if sign > 0 else p - scale * force
 
 
-def euler_step(x, f, sign):
-    """x + sign * f (state dtype = x's)."""
+def euler_step(x, f, sign, graph_only=False):
+    """x + sign * f (state dtype = x's); ``graph_only`` as midpoint_step's."""
     if x.device.type == "cuda":
-        return EulerStep.apply(x, f, sign)
+        return EulerStep.apply(x, f, sign, graph_only)
     return x + f if sign > 0 else x - f

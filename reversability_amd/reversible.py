@@ -70,7 +70,8 @@ def _euler_inverse_for_vjp(block, p, q):
     """Invert one Euler step and rebuild its graph with one evaluation of
     A(p0): p0 = p - M(q) (no graph), a = A(p0) with its graph, q0 = q - a, then
     next_q = q0 + a and next_p = p0 + M(next_q) as forward_pair computes them.
-    Returns (next_p, next_q, p0, q0) with p0, q0 the graph's leaves."""
+    Returns (next_p, next_q, p0, q0) with p0, q0 the graph's leaves; next_p is
+    for differentiation only (on the GPU its value is not computed)."""
     with torch.no_grad():
         p0 = euler_step(p, block.mlp(block.mlp_norm(q)), -1)
     with torch.enable_grad():
@@ -83,7 +84,8 @@ def _euler_inverse_for_vjp(block, p, q):
             q0 = euler_step(q, attention.detach(), -1)
         q0 = q0.detach().requires_grad_(True)
         next_q, normed = add_rms_norm(q0, attention, block.mlp_norm)
-        next_p = euler_step(p0_pass, block.mlp(normed), +1)
+        # next_p is only differentiated (its value is never read)
+        next_p = euler_step(p0_pass, block.mlp(normed), +1, graph_only=True)
     return next_p, next_q, p0, q0
 
 
