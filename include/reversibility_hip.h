@@ -178,6 +178,16 @@ int rv_rmsnorm_bwd_acc(const float* x, const float* w, const void* dy, int dy_dt
                        void* workspace, int64_t workspace_bytes, int64_t rows, int64_t width,
                        void* stream);
 
+/* rv_rmsnorm_bwd_acc for an input that also passes through unchanged to
+ * another use (the split midpoint's q, an output of the rebuilt step as well
+ * as the residual input of the add): dx16 = fp16(norm backward) (the force
+ * term's gradient) and dx = norm backward + dpass (the input's total, the sum
+ * autograd would form).  Requires dx16 and no dh. */
+int rv_rmsnorm_bwd_acc_pass(const float* x, const float* w, const void* dy, int dy_dtype,
+                            const float* rstd, const float* dh, const float* dpass, float* dx,
+                            void* dx16, float* dw, void* workspace, int64_t workspace_bytes,
+                            int64_t rows, int64_t width, void* stream);
+
 /* Fused residual add + RMSNorm (the x + A(x) -> mlp_norm step of
  * midpoint_force and the q' = q + A(p) -> mlp_norm step of Euler):
  *   h[r, :] = x[r, :] + S(f[r, :])             (written to h)

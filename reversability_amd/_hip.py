@@ -72,6 +72,8 @@ SIGNATURES = {
     "rv_gemm_force_shape": (_I, [_I]),
     "rv_add_rmsnorm_fwd_f16": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_rmsnorm_bwd_acc": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rv_rmsnorm_bwd_acc_pass": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                     _I64, _P]),
     "rv_ce_fused": (_I, [_P, _I, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "rv_mlp_up_swiglu": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "rv_mlp_down": (_I, [_P, _P, _I64, _I64, _I64, _P, _P]),
@@ -252,7 +254,8 @@ def _add_rmsnorm_fwd16(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: f
 
 
 def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.Tensor,
-                     dh: Optional[torch.Tensor], f16: bool = True):
+                     dh: Optional[torch.Tensor], f16: bool = True,
+                     dpass: Optional[torch.Tensor] = None):
     width = x.shape[-1]
     rows = x.numel() // width if width else 0
     dx = torch.empty_like(x)
@@ -264,9 +267,10 @@ def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: t
     nbytes = rmsnorm_workspace_bytes(rows, width)
     ws = torch.empty(nbytes // 4, device=x.device, dtype=torch.float32)
     with _DeviceGuard(x):
-        _check(library().rv_rmsnorm_bwd_acc(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
+        _check(library().rv_rmsnorm_bwd_acc_pass(x.data_ptr(), w.data_ptr(), dy.data_ptr(),
                                             _dtype_code(dy), rstd.data_ptr(),
                                             dh.data_ptr() if dh is not None else None,
+                                            dpass.data_ptr() if dpass is not None else None,
                                             dx.data_ptr(), dx16.data_ptr() if f16 else None,
                                             dw.data_ptr(),
                                             ws.data_ptr(), nbytes, rows, width, _stream(x)),
@@ -378,7 +382,8 @@ _SCHEMAS = {
     "add_rmsnorm_fwd16": ("add_rmsnorm_fwd16(Tensor x, Tensor f, Tensor weight, float eps) "
                           "-> (Tensor, Tensor, Tensor)", _add_rmsnorm_fwd16),
     "rmsnorm_bwd_acc": ("rmsnorm_bwd_acc(Tensor x, Tensor weight, Tensor dy, Tensor rstd, "
-                        "Tensor? dh, bool f16=True) -> (Tensor, Tensor, Tensor)",
+                        "Tensor? dh, bool f16=True, Tensor? dpass=None) "
+                        "-> (Tensor, Tensor, Tensor)",
                         _rmsnorm_bwd_acc),
     "swiglu_fwd": ("swiglu_fwd(Tensor u) -> Tensor", _swiglu_fwd),
     "swiglu_bwd": ("swiglu_bwd(Tensor u, Tensor dy) -> Tensor", _swiglu_bwd),
@@ -425,7 +430,7 @@ def _(x, f, weight, eps):
 
 
 @torch.library.register_fake(f"{NAMESPACE}::rmsnorm_bwd_acc")
-def _(x, weight, dy, rstd, dh, f16=True):
+def _(x, weight, dy, rstd, dh, f16=True, dpass=None):
     return (torch.empty_like(x), torch.empty_like(x, dtype=torch.float16) if f16
             else x.new_empty(0, dtype=torch.float16), torch.empty_like(weight))
 

@@ -243,18 +243,23 @@ void rms_fwd_scalar(const float* __restrict__ x, const F* __restrict__ f,
 // ---------------------------------------------------------------------------
 // ACC: the row gradient also receives dh (the gradient of the normalized
 // input's other use: dx = dh + norm backward, the sum autograd would form).
-template <int VEC, bool ACC>
+// PASS: the input also has a pass-through use whose gradient dpass joins dx
+// after the fp16 copy (that copy is the force term's gradient, which does not
+// include it).
+template <int VEC, bool ACC, bool PASS = false>
 struct BwdTile {
   float4 x[2][VEC], g[2][VEC];
   float4 h[ACC ? 2 : 1][ACC ? VEC : 1];
+  float4 p[PASS ? 2 : 1][PASS ? VEC : 1];
   float rs[2];
 };
 
-template <int VEC, bool ACC, typename G>
-__device__ __forceinline__ void bwd_load(BwdTile<VEC, ACC>& t, const float* __restrict__ x,
+template <int VEC, bool ACC, bool PASS, typename G>
+__device__ __forceinline__ void bwd_load(BwdTile<VEC, ACC, PASS>& t, const float* __restrict__ x,
                                          const G* __restrict__ dy,
                                          const float* __restrict__ rstd,
-                                         const float* __restrict__ dh, int64_t row0,
+                                         const float* __restrict__ dh,
+                                         const float* __restrict__ dpass, int64_t row0,
                                          int64_t end, int width, int lane) {
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -267,12 +272,13 @@ __device__ __forceinline__ void bwd_load(BwdTile<VEC, ACC>& t, const float* __re
       t.x[r][v] = rv::ld_f4(x + row * width + col_c);
       t.g[r][v] = rv::load4f(dy + row * width + col_c);
       if constexpr (ACC) t.h[r][v] = rv::ld_f4(dh + row * width + col_c);
+      if constexpr (PASS) t.p[r][v] = rv::ld_f4(dpass + row * width + col_c);
     }
   }
 }
 
-template <int VEC, bool ACC, bool H16>
-__device__ __forceinline__ void bwd_finish(BwdTile<VEC, ACC>& t, const float4 (&wv)[VEC],
+template <int VEC, bool ACC, bool H16, bool PASS>
+__device__ __forceinline__ void bwd_finish(BwdTile<VEC, ACC, PASS>& t, const float4 (&wv)[VEC],
                                            float4 (&acc)[VEC], float* __restrict__ dx,
                                            __half* __restrict__ dx16,
                                            int64_t row0, int64_t end, int width, int lane) {
@@ -321,8 +327,14 @@ __device__ __forceinline__ void bwd_finish(BwdTile<VEC, ACC>& t, const float4 (&
           o.z = o.z + t.h[r][v].z;
           o.w = o.w + t.h[r][v].w;
         }
-        rv::st_f4s(dx + row * width + col, o);
         if constexpr (H16) store_y(dx16 + row * width + col, o);
+        if constexpr (PASS) {
+          o.x = o.x + t.p[r][v].x;
+          o.y = o.y + t.p[r][v].y;
+          o.z = o.z + t.p[r][v].z;
+          o.w = o.w + t.p[r][v].w;
+        }
+        rv::st_f4s(dx + row * width + col, o);
       }
     }
   }
@@ -330,13 +342,14 @@ __device__ __forceinline__ void bwd_finish(BwdTile<VEC, ACC>& t, const float4 (&
 
 // WAVES per block: wide rows keep fewer waves so that their two-row
 // ping-pong tiles stay in registers (no scratch).
-template <int VEC, int WAVES, typename G, bool ACC = false, bool H16 = false>
+template <int VEC, int WAVES, typename G, bool ACC = false, bool H16 = false, bool PASS = false>
 __global__ __launch_bounds__(WAVES * 64)
 void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
                  const G* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
                  int64_t rows, int width, int64_t rows_per_block,
-                 const float* __restrict__ dh = nullptr, __half* __restrict__ dx16 = nullptr) {
+                 const float* __restrict__ dh = nullptr, __half* __restrict__ dx16 = nullptr,
+                 const float* __restrict__ dpass = nullptr) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t start = (int64_t)blockIdx.x * rows_per_block;
@@ -356,15 +369,15 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
   if (first < end) {  // wave-uniform
     const int64_t iters = (end - 1 - first) / stride + 1;
     int64_t row0 = first;
-    BwdTile<VEC, ACC> a, b;
-    bwd_load(a, x, dy, rstd, dh, row0, end, width, lane);
+    BwdTile<VEC, ACC, PASS> a, b;
+    bwd_load(a, x, dy, rstd, dh, dpass, row0, end, width, lane);
     for (int64_t k = 0; k < iters; k += 2) {
-      bwd_load(b, x, dy, rstd, dh, row0 + stride, end, width, lane);
-      bwd_finish<VEC, ACC, H16>(a, wv, acc, dx, dx16, row0, end, width, lane);
+      bwd_load(b, x, dy, rstd, dh, dpass, row0 + stride, end, width, lane);
+      bwd_finish<VEC, ACC, H16, PASS>(a, wv, acc, dx, dx16, row0, end, width, lane);
       if (k + 1 >= iters) break;
       row0 += stride;
-      bwd_load(a, x, dy, rstd, dh, row0 + stride, end, width, lane);
-      bwd_finish<VEC, ACC, H16>(b, wv, acc, dx, dx16, row0, end, width, lane);
+      bwd_load(a, x, dy, rstd, dh, dpass, row0 + stride, end, width, lane);
+      bwd_finish<VEC, ACC, H16, PASS>(b, wv, acc, dx, dx16, row0, end, width, lane);
       row0 += stride;
     }
   }
@@ -565,7 +578,7 @@ template <typename G>
 int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, float* dx,
                float* dw, void* workspace, int64_t workspace_bytes, int64_t rows,
                int64_t width, hipStream_t s, const float* dh = nullptr,
-               __half* dx16 = nullptr) {
+               __half* dx16 = nullptr, const float* dpass = nullptr) {
   if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > 4096) return RV_ERR_UNSUPPORTED;
@@ -581,17 +594,24 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
                    rv_host::aligned16(w) &&
                    (reinterpret_cast<uintptr_t>(dy) % (4 * sizeof(G))) == 0 &&
                    rv_host::aligned16(dx) && (dh == nullptr || rv_host::aligned16(dh)) &&
+                   (dpass == nullptr || rv_host::aligned16(dpass)) &&
                    (reinterpret_cast<uintptr_t>(dx16) % 8) == 0;
-  if (!vec && (dh != nullptr || dx16 != nullptr)) return RV_ERR_UNSUPPORTED;
+  if (!vec && (dh != nullptr || dx16 != nullptr || dpass != nullptr)) return RV_ERR_UNSUPPORTED;
+  // the pass-through gradient: with the fp16 copy and without dh only
+  if (dpass != nullptr && (dh != nullptr || dx16 == nullptr)) return RV_ERR_UNSUPPORTED;
   if (vec) {
     const int vecs = (iw + 255) / 256;
 #define RV_BWD_VEC_K(V, ACC, H16)                                                         \
   hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V, ACC), G, ACC, H16>), grid,              \
                      dim3(bwd_waves(V, ACC) * 64), 0, s, x, w, dy, rstd, dx, partial, rows,  \
-                     iw, p.rows_per_block, dh, dx16)
+                     iw, p.rows_per_block, dh, dx16, nullptr)
 #define RV_BWD_VEC(V)                                                \
   do {                                                               \
-    if (dh != nullptr && dx16 != nullptr) RV_BWD_VEC_K(V, true, true);   \
+    if (dpass != nullptr)                                            \
+      hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V, true), G, false, true, true>), grid, \
+                         dim3(bwd_waves(V, true) * 64), 0, s, x, w, dy, rstd, dx, partial, \
+                         rows, iw, p.rows_per_block, nullptr, dx16, dpass);          \
+    else if (dh != nullptr && dx16 != nullptr) RV_BWD_VEC_K(V, true, true);   \
     else if (dh != nullptr) RV_BWD_VEC_K(V, true, false);            \
     else if (dx16 != nullptr) RV_BWD_VEC_K(V, false, true);          \
     else RV_BWD_VEC_K(V, false, false);                              \
@@ -716,15 +736,23 @@ int rv_rmsnorm_bwd_acc(const float* x, const float* w, const void* dy, int dy_dt
                        const float* rstd, const float* dh, float* dx, void* dx16, float* dw,
                        void* workspace, int64_t workspace_bytes, int64_t rows, int64_t width,
                        void* stream) {
+  return rv_rmsnorm_bwd_acc_pass(x, w, dy, dy_dtype, rstd, dh, nullptr, dx, dx16, dw, workspace,
+                                 workspace_bytes, rows, width, stream);
+}
+
+int rv_rmsnorm_bwd_acc_pass(const float* x, const float* w, const void* dy, int dy_dtype,
+                            const float* rstd, const float* dh, const float* dpass, float* dx,
+                            void* dx16, float* dw, void* workspace, int64_t workspace_bytes,
+                            int64_t rows, int64_t width, void* stream) {
   const hipStream_t s = (hipStream_t)stream;
   __half* d16 = static_cast<__half*>(dx16);
   switch (dy_dtype) {
     case RV_F32:
       return launch_bwd<float>(x, w, static_cast<const float*>(dy), rstd, dx, dw, workspace,
-                               workspace_bytes, rows, width, s, dh, d16);
+                               workspace_bytes, rows, width, s, dh, d16, dpass);
     case RV_F16:
       return launch_bwd<__half>(x, w, static_cast<const __half*>(dy), rstd, dx, dw, workspace,
-                                workspace_bytes, rows, width, s, dh, d16);
+                                workspace_bytes, rows, width, s, dh, d16, dpass);
     default:
       return RV_ERR_UNSUPPORTED;
   }

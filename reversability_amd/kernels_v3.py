@@ -138,6 +138,49 @@ def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module):
     return x, norm(x)
 
 
+class FusedAddRMSNormPass(torch.autograd.Function):
+    """FusedAddRMSNorm whose residual input x also passes through unchanged as a
+    third output (the split midpoint's q: an output of the rebuilt step and
+    the input of ``q + proxy``): backward sums x's gradients -- the norm's and
+    the pass-through's -- in the norm's backward pass
+    (``rv_rmsnorm_bwd_acc_pass``); the force term's fp16 gradient excludes the
+    pass-through share.  The sum's other output h must have no other use."""
+
+    @staticmethod
+    def forward(ctx, x, f, weight, eps):
+        ctx.set_materialize_grads(False)
+        h, y, rstd = ops.add_rmsnorm_fwd16(x, f, weight.contiguous(), float(eps))
+        ctx.save_for_backward(h, weight, rstd)
+        ctx.f_dtype = f.dtype
+        return x.view_as(x), y
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dpass, dy):
+        h, weight, rstd = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(h, dtype=torch.float16)
+        elif dy.dtype not in (torch.float32, torch.float16):
+            dy = dy.float()
+        dpass = dpass.contiguous() if dpass is not None else None
+        dx, dx16, dweight = ops.rmsnorm_bwd_acc(h, weight.contiguous(), dy.contiguous(), rstd,
+                                                None, True, dpass)
+        df = dx16 if ctx.f_dtype == torch.float16 else dx.to(ctx.f_dtype)
+        return dx, df, dweight, None
+
+
+def add_rms_norm_pass(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
+    """``(x', norm(x + f))`` for a residual input x with a pass-through use x'
+    (and no other use of the sum), on the fused kernels where ``add_rms_norm``
+    would take them (f fp16 there); otherwise ``(x, norm(x + f))``."""
+    if (getattr(norm, "_rv_fp16_out", False) and x.is_cuda and x.dtype == torch.float32
+            and f.dtype == torch.float16 and x.shape == f.shape
+            and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
+            and _fp16_out(x)):
+        return FusedAddRMSNormPass.apply(x, f, norm.weight, rms_norm_eps(norm, x))
+    return x.view_as(x), add_rms_norm(x, f, norm)[1]
+
+
 def add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
     """``(h, norm(h))`` with ``h = x + f``.  On the fused kernels when ``norm``
     is an RMSNorm routed by ``enable_rmsnorm(..., fp16_out=True)`` and the

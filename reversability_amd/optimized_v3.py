@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
-from .kernels_v3 import add_rms_norm, rms_norm_pass
+from .kernels_v3 import add_rms_norm, add_rms_norm_pass, rms_norm_pass
 from .optimized import ReusedMidpoint, amp_context, hidden_states
 from .residual import midpoint_step
 
@@ -237,19 +237,22 @@ class SplitMidpoint(torch.autograd.Function):
                 with torch.enable_grad():
                     previous_q = p.detach().requires_grad_(True)
                     proxy = attention.detach().requires_grad_(True)
-                    mlp = block.mlp(add_rms_norm(previous_q, proxy, block.mlp_norm)[1])
+                    # previous_q is also an output of this step: its two
+                    # gradients are summed in the norm's backward pass
+                    q_pass, mlp_in = add_rms_norm_pass(previous_q, proxy, block.mlp_norm)
+                    mlp = block.mlp(mlp_in)
                     with torch.no_grad():
                         previous_p = midpoint_step(q, proxy.detach(), mlp.detach(), scale, -1)
                     previous_p.requires_grad_(True)
                     # only differentiated: its value is never read
                     next_q = midpoint_step(previous_p, proxy, mlp, scale, +1, graph_only=True)
                     mlp_parameters = (*block.mlp_norm.parameters(), *block.mlp.parameters())
-                    local = torch.autograd.grad((previous_q, next_q),
+                    local = torch.autograd.grad((q_pass, next_q),
                                                 (previous_p, previous_q, proxy, *mlp_parameters),
                                                 (dp, dq))
                 next_dp, q_mlp, attention_cotangent = local[:3]
                 mlp_grads = local[3:]
-                del proxy, mlp, next_q, local
+                del proxy, mlp, next_q, local, q_pass, mlp_in
                 with torch.enable_grad():
                     if not KEEP_SPLIT_ATTENTION:
                         attn_input = previous_q.detach().requires_grad_(True)

@@ -364,3 +364,36 @@ def test_rmsnorm_pass_matches_composition(cuda_device, rows, width, fp16_out):
         assert torch.allclose(dw1, dw2, rtol=1e-5, atol=1e-6)
     else:
         assert torch.equal(dw1, dw2)
+
+
+@pytest.mark.parametrize("rows,width", [(1000, 256), (300, 1024)])
+def test_fused_add_rmsnorm_pass_matches_composition(cuda_device, rows, width):
+    """FusedAddRMSNormPass = (x as a second use, FusedRMSNorm(x + f)) with
+    autograd's sum of x's gradients and the fp16 cast of f's: y, dx, df bit
+    for bit; dweight too at width 256 (at 1024 the accumulating backward's
+    fewer waves sum it in another fixed order: within fp32 summation error)."""
+    from reversability_amd.kernels_v3 import FusedAddRMSNormPass
+    from reversability_amd.residual import euler_step
+    g = torch.Generator().manual_seed(rows + 7 * width)
+    x0 = torch.randn(rows, width, generator=g).to(cuda_device)
+    f0 = torch.randn(rows, width, generator=g).half().to(cuda_device)
+    w0 = (1 + 0.02 * torch.randn(width, generator=g)).to(cuda_device)
+    gy = torch.randn(rows, width, generator=g).half().to(cuda_device)
+    gp = torch.randn(rows, width, generator=g).to(cuda_device)
+    eps = float(torch.finfo(torch.float32).eps)
+    outs = []
+    for fused in (True, False):
+        x, f, w = (t.clone().requires_grad_(True) for t in (x0, f0, w0))
+        with torch.autocast("cuda", dtype=torch.float16):
+            if fused:
+                xp, y = FusedAddRMSNormPass.apply(x, f, w, eps)
+            else:
+                xp, y = x, FusedRMSNorm.apply(euler_step(x, f, +1), w, eps, True)
+        ((y.float() * gy.float()).sum() + (xp * gp).sum()).backward()
+        outs.append((y.detach(), x.grad, f.grad, w.grad))
+    for i, (a, b) in enumerate(zip(*outs)):
+        assert a.dtype == b.dtype
+        if i == 3 and width > 256:
+            assert torch.allclose(a, b, rtol=1e-5, atol=1e-6)
+        else:
+            assert torch.equal(a, b), i
