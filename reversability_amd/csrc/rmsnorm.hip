@@ -467,10 +467,12 @@ void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
 
 // dw[col] = sum over parts of partial[part][col] (row-major, one contiguous
 // row per backward block).  A block covers 64 columns (lane = column) with
-// kRedWaves waves; wave k sums parts k, k + kRedWaves, ... in order (their
-// loads are independent, so a wave issues them all before adding), then the
-// waves' sums are added in wave order through LDS.  Fixed order throughout.
+// kRedWaves waves; wave k sums parts k, k + kRedWaves, ... in order (all of
+// its at most kRedPerWave loads are issued before the first add: one memory
+// round trip), then the waves' sums are added in wave order through LDS.
+// Fixed order throughout.
 constexpr int kRedWaves = 16;
+constexpr int kRedPerWave = 16;  // parts per wave: nparts <= kRedWaves * kRedPerWave
 
 __global__ __launch_bounds__(kRedWaves * 64)
 void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
@@ -479,10 +481,16 @@ void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
   const int wave = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
   const int col_c = col < width ? col : width - 1;
+  float v[kRedPerWave];
+#pragma unroll
+  for (int i = 0; i < kRedPerWave; ++i) {
+    const int part = wave + i * kRedWaves;
+    v[i] = partial[(int64_t)(part < nparts ? part : nparts - 1) * width + col_c];
+  }
   float s = 0.f;
-#pragma unroll 8
-  for (int part = wave; part < nparts; part += kRedWaves)
-    s = s + partial[(int64_t)part * width + col_c];
+#pragma unroll
+  for (int i = 0; i < kRedPerWave; ++i)
+    if (wave + i * kRedWaves < nparts) s = s + v[i];
   __shared__ float red[kRedWaves][64];
   red[wave][lane] = s;
   __syncthreads();
@@ -511,6 +519,8 @@ struct BwdPlan {
 // back the per-XCD L2 on MI355X and measured 4-15x slower than this second
 // launch.)
 constexpr int64_t kBwdTargetBlocks = RV_RMS_BWD_BLOCKS;
+static_assert(kBwdTargetBlocks <= kRedWaves * kRedPerWave,
+              "rms_dw_reduce sums at most kRedWaves * kRedPerWave partial rows");
 
 BwdPlan plan_bwd(int64_t rows) {
   const int64_t target = kBwdTargetBlocks;
