@@ -291,6 +291,31 @@ def test_residual_axpy_bitwise(cuda_device, sign):
     assert np.array_equal(out.numpy(), oracle.euler(x.numpy(), f.numpy(), sign))
 
 
+@pytest.mark.parametrize("sign", [1, -1])
+def test_graph_only_residual_steps_have_the_same_gradients(cuda_device, sign):
+    """A residual step built with graph_only=True (value not evaluated) back-
+    propagates exactly what the evaluated step does, for the Euler and the
+    midpoint update, through a downstream op that reads the input too."""
+    from reversability_amd.residual import euler_step, midpoint_step
+    g = gen(29)
+    x = torch.randn(333, 256, generator=g).to(cuda_device)
+    a = torch.randn(333, 256, generator=g).half().to(cuda_device)
+    m = torch.randn(333, 256, generator=g).half().to(cuda_device)
+    dout = torch.randn(333, 256, generator=g).to(cuda_device)
+
+    def grads(step):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (x, a, m)]
+        out = step(*leaves)
+        torch.autograd.backward((out, leaves[0] * 3.0), (dout, dout))
+        return [t.grad for t in leaves]
+
+    for build in (lambda gonly: lambda p, f, h: euler_step(p, f + h, sign, graph_only=gonly),
+                  lambda gonly: lambda p, f, h: midpoint_step(p, f, h, 0.5, sign,
+                                                              graph_only=gonly)):
+        for got, ref in zip(grads(build(True)), grads(build(False))):
+            assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("rows,width,f_dtype,use_h", [(1000, 256, torch.float16, True),
                                                       (777, 1024, torch.float16, False),
                                                       (777, 1024, torch.float16, True),
