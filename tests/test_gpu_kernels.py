@@ -291,6 +291,30 @@ def test_residual_axpy_bitwise(cuda_device, sign):
     assert np.array_equal(out.numpy(), oracle.euler(x.numpy(), f.numpy(), sign))
 
 
+def test_empty_inputs_match_eager(cuda_device):
+    """Zero rows through the autograd Functions: the same shapes and gradients
+    as eager torch (dweight zero, no kernel launched)."""
+    from reversability_amd.residual import euler_step, midpoint_step
+    eps = float(torch.finfo(torch.float32).eps)
+    x = torch.zeros(0, 256, device=cuda_device, requires_grad=True)
+    w = torch.ones(256, device=cuda_device, requires_grad=True)
+    y = FusedRMSNorm.apply(x, w, eps)
+    assert y.shape == (0, 256)
+    y.sum().backward()
+    assert x.grad.shape == (0, 256) and torch.equal(w.grad, torch.zeros_like(w))
+    for dtype in (torch.float16, torch.float32):
+        u = torch.zeros(2, 0, 2048, device=cuda_device, dtype=dtype, requires_grad=True)
+        o = FusedSwiGLU.apply(u)
+        ref = F.silu(u[..., :1024]) * u[..., 1024:]
+        assert o.shape == ref.shape and o.dtype == ref.dtype
+        o.sum().backward()
+        assert u.grad.shape == u.shape
+    p = torch.zeros(0, 256, device=cuda_device)
+    f = torch.zeros(0, 256, device=cuda_device, dtype=torch.float16)
+    assert euler_step(p, f, +1).shape == (0, 256)
+    assert midpoint_step(p, f, f, 0.5, -1).shape == (0, 256)
+
+
 @pytest.mark.parametrize("sign", [1, -1])
 def test_graph_only_residual_steps_have_the_same_gradients(cuda_device, sign):
     """A residual step built with graph_only=True (value not evaluated) back-
