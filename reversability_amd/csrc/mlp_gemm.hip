@@ -578,11 +578,25 @@ template __global__ void gemm_kernel<256, 256, false, true, Epi::StoreF16, 8>(Ge
 
 // acc[i] (+)= fp32(fp16(sum_s part[s][i])), splits summed in order.  This is
 // autocast's weight gradient: the fp16 GEMM result, cast to the fp32 weight
-// and added to the running per-tile sum.  n % 4 == 0.
+// and added to the running per-tile sum.  n % 4 == 0.  One launch finishes up
+// to two weight gradients: blocks [0, a.blocks) reduce segment a, the rest b.
+struct ReduceSeg {
+  const float* part;
+  float* out;
+  int64_t n;
+  int splits;
+  int64_t blocks;  // 0: nothing to reduce
+};
+
 __global__ __launch_bounds__(256)
-void wgrad_reduce(const float* __restrict__ part, int splits, int64_t n, float* __restrict__ out,
-                  int accumulate) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+void wgrad_reduce(ReduceSeg a, ReduceSeg b, int accumulate) {
+  const bool second = (int64_t)blockIdx.x >= a.blocks;
+  const float* part = second ? b.part : a.part;
+  float* out = second ? b.out : a.out;
+  const int64_t n = second ? b.n : a.n;
+  const int splits = second ? b.splits : a.splits;
+  const int64_t blk = second ? (int64_t)blockIdx.x - a.blocks : (int64_t)blockIdx.x;
+  const int64_t i = (blk * 256 + threadIdx.x) * 4;
   if (i >= n) return;
   float4 s = *reinterpret_cast<const float4*>(part + i);
   for (int k = 1; k < splits; ++k) {
@@ -838,8 +852,13 @@ WgradPlan plan_wgrad(int64_t rows, int64_t ni, int64_t nj) {
   return best;
 }
 
-int run_wgrad(const __half* a, int64_t lda, const __half* b, int64_t ldb, int64_t rows,
-              int64_t ni, int64_t nj, float* out, int accumulate, float* part, hipStream_t s) {
+// The weight-gradient GEMM.  Unsplit, it writes (or adds) the result itself;
+// split, its fp32 partial sums go to `part` and `seg` describes the reduction
+// still to launch (seg.blocks == 0 otherwise).
+int launch_wgrad(const __half* a, int64_t lda, const __half* b, int64_t ldb, int64_t rows,
+                 int64_t ni, int64_t nj, float* out, int accumulate, float* part,
+                 ReduceSeg& seg, hipStream_t s) {
+  seg = ReduceSeg{nullptr, nullptr, 0, 0, 0};
   const WgradPlan p = plan_wgrad(rows, ni, nj);
   if (p.shape < 0) return RV_ERR_UNSUPPORTED;
   GemmArgs g{};
@@ -853,12 +872,26 @@ int run_wgrad(const __half* a, int64_t lda, const __half* b, int64_t ldb, int64_
     return launch<true, true, Epi::AccF32OfF16>(p.shape, g, 1, s);
   }
   g.c = part;
-  int st = launch<true, true, Epi::PartialF32>(p.shape, g, p.splits, s);
+  const int st = launch<true, true, Epi::PartialF32>(p.shape, g, p.splits, s);
   if (st != RV_OK) return st;
   const int64_t n = ni * nj;
-  hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, part,
-                     (int)p.splits, n, out, accumulate);
+  seg = ReduceSeg{part, out, n, (int)p.splits, (n / 4 + 255) / 256};
+  return RV_OK;
+}
+
+int launch_reduce(const ReduceSeg& a, const ReduceSeg& b, int accumulate, hipStream_t s) {
+  const int64_t blocks = a.blocks + b.blocks;
+  if (blocks == 0) return RV_OK;
+  hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)blocks), dim3(256), 0, s, a, b, accumulate);
   return rv_host::check_launch();
+}
+
+int run_wgrad(const __half* a, int64_t lda, const __half* b, int64_t ldb, int64_t rows,
+              int64_t ni, int64_t nj, float* out, int accumulate, float* part, hipStream_t s) {
+  ReduceSeg seg;
+  const int st = launch_wgrad(a, lda, b, ldb, rows, ni, nj, out, accumulate, part, seg, s);
+  if (st != RV_OK) return st;
+  return launch_reduce(seg, ReduceSeg{nullptr, nullptr, 0, 0, 0}, accumulate, s);
 }
 
 int64_t wgrad_part_bytes(int64_t rows, int64_t ni, int64_t nj) {
@@ -868,6 +901,8 @@ int64_t wgrad_part_bytes(int64_t rows, int64_t ni, int64_t nj) {
 }
 
 bool ok16(const void* p) { return rv_host::aligned16(p); }
+
+int64_t align256(int64_t bytes) { return (bytes + 255) & ~(int64_t)255; }
 
 // Buffer loads address an operand with 32-bit byte offsets.
 bool fits32(int64_t elems) { return elems > 0 && elems * 2 <= (int64_t)INT32_MAX - (int64_t)(1 << 24); }
@@ -1047,7 +1082,7 @@ int64_t rv_mlp_wgrad_workspace_bytes(int64_t rows, int64_t d, int64_t f) {
   if (rows <= 0 || d <= 0 || f <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
   const int64_t a = wgrad_part_bytes(rows, d, f), b = wgrad_part_bytes(rows, 2 * f, d);
   if (a < 0 || b < 0) return -(int64_t)RV_ERR_UNSUPPORTED;
-  return a > b ? a : b;
+  return (b > 0 ? align256(a) : a) + b;  // both partial sets at once (one reduction launch)
 }
 
 int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x, int64_t ldx,
@@ -1064,14 +1099,19 @@ int rv_mlp_wgrad(const void* dy, const void* o, const void* du, const void* x, i
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !ok16(workspace)))
     return RV_ERR_WORKSPACE;
   const hipStream_t s = (hipStream_t)stream;
-  float* part = static_cast<float*>(workspace);
+  // the two GEMMs' partial sums side by side, reduced by one launch
+  float* part_down = static_cast<float*>(workspace);
+  float* part_up = part_down + align256(wgrad_part_bytes(rows, d, f)) / (int64_t)sizeof(float);
+  ReduceSeg seg_down, seg_up;
   // dW_down[d][f] = sum_m dy[m][d] o[m][f]
-  int st = run_wgrad(static_cast<const __half*>(dy), d, static_cast<const __half*>(o), f, rows,
-                     d, f, ddown, accumulate, part, s);
+  int st = launch_wgrad(static_cast<const __half*>(dy), d, static_cast<const __half*>(o), f, rows,
+                        d, f, ddown, accumulate, part_down, seg_down, s);
   if (st != RV_OK) return st;
   // dW_up[2f][d] = sum_m du[m][j] x16[m][d]
-  return run_wgrad(static_cast<const __half*>(du), 2 * f, static_cast<const __half*>(x), ldx,
-                   rows, 2 * f, d, dup, accumulate, part, s);
+  st = launch_wgrad(static_cast<const __half*>(du), 2 * f, static_cast<const __half*>(x), ldx,
+                    rows, 2 * f, d, dup, accumulate, part_up, seg_up, s);
+  if (st != RV_OK) return st;
+  return launch_reduce(seg_down, seg_up, accumulate, s);
 }
 
 }  // extern "C"
