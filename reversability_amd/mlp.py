@@ -51,6 +51,29 @@ def cast_f16(t: torch.Tensor) -> torch.Tensor:
 # Call-scoped cache of fp16 weight casts (see weight_cast_cache).
 _weight_cache: dict | None = None
 
+# Depth of output_unused blocks currently open.
+_output_unused = 0
+
+
+@contextlib.contextmanager
+def output_unused():
+    """Inside this block the tiled MLP's output is only differentiated, never
+    read: ``install_v3``'s MLP forward on a GPU tensor keeps its tiles for the
+    backward but skips the down projection (the output tensor is allocated,
+    not computed).  For an MLP evaluation that only feeds a rebuilt
+    ``graph_only`` residual step.  The backward is unchanged."""
+    global _output_unused
+    _output_unused += 1
+    try:
+        yield
+    finally:
+        _output_unused -= 1
+
+
+def output_wanted(x: torch.Tensor) -> bool:
+    """False inside ``output_unused`` for a GPU input."""
+    return not (_output_unused and x.is_cuda)
+
 
 @contextlib.contextmanager
 def weight_cast_cache():

@@ -100,7 +100,7 @@ class TiledMLP(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, up, down, tokens, fused, keep_tiles=False):
+    def forward(ctx, x, up, down, tokens, fused, keep_tiles=False, need_output=True):
         if tokens < 1:
             raise ValueError("Positive MLP tile size required")
         ctx.tokens, ctx.fused = tokens, fused
@@ -120,7 +120,8 @@ class TiledMLP(torch.autograd.Function):
             tiles = [] if keep_tiles else None
             for start in range(0, flat.shape[0], tokens):
                 o, u = mlp.up_swiglu(x16[start:start + tokens], up16, keep_u=keep_tiles)
-                mlp.down(o, down16, output[start:start + tokens])
+                if need_output:
+                    mlp.down(o, down16, output[start:start + tokens])
                 if keep_tiles:
                     tiles.append((o, u))
             ctx.tiles = tiles
@@ -132,8 +133,10 @@ class TiledMLP(torch.autograd.Function):
             # call here gives the same values
             up_c, down_c = up.to(cdt), down.to(cdt)
             for start in range(0, flat.shape[0], tokens):
-                *_, y = tile_forward(flat[start:start + tokens], up_c, down_c, fused, cdt)
-                output[start:start + tokens].copy_(y)
+                *_, y = tile_forward(flat[start:start + tokens], up_c, down_c, fused, cdt,
+                                     need_output=need_output)
+                if need_output:
+                    output[start:start + tokens].copy_(y)
         ctx.save_for_backward(x, up, down)
         return output.reshape(*x.shape[:-1], down.shape[0])
 
@@ -163,7 +166,7 @@ class TiledMLP(torch.autograd.Function):
                 mlp.dx(du, up16, dx[start:stop])
                 mlp.wgrad(g, o, du, x_t, ddown, dup, accumulate=i > 0)
                 del o, u, du
-            return dx.reshape_as(x), dup, ddown, None, None, None
+            return dx.reshape_as(x), dup, ddown, None, None, None, None
         dup = ddown = None
         with torch.autocast(ctx.device, enabled=False):
             up_c, down_c = up.to(cdt), down.to(cdt)
@@ -183,7 +186,7 @@ class TiledMLP(torch.autograd.Function):
                 del x_c, u, o, g, d_o, du, tile_ddown, tile_dup
         if dup is None:  # no rows
             dup, ddown = torch.zeros_like(up), torch.zeros_like(down)
-        return dx.reshape_as(x), dup, ddown, None, None, None
+        return dx.reshape_as(x), dup, ddown, None, None, None, None
 
 
 # SplitMidpoint's backward evaluates each layer's attention twice on the same
@@ -347,8 +350,10 @@ def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsn
                 raise ValueError("Tiled MLP experiment supports frozen bias=False only")
 
             def forward(self, x):
+                from . import mlp
                 return TiledMLP.apply(x, self.up.weight, self.down.weight, mlp_tokens, swiglu,
-                                      keep_mlp_tiles and torch.is_grad_enabled())
+                                      keep_mlp_tiles and torch.is_grad_enabled(),
+                                      mlp.output_wanted(x))
             block.mlp.forward = types.MethodType(forward, block.mlp)
     elif swiglu:
         from .kernels import enable_swiglu

@@ -19,12 +19,14 @@ expression's rounding points.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
 from torch.autograd.function import once_differentiable
 
 from .kernels_v3 import add_rms_norm, rms_norm_pass
+from .mlp import output_unused
 from .model import BaselineLM, Block, ModelConfig
 from .residual import euler_step, midpoint_step
 
@@ -65,6 +67,10 @@ def inverse_pair(block, p, q, method, h):
 # With this set the inversion keeps that evaluation's graph for the VJP.
 REUSE_EULER_ATTENTION = True
 
+# The Euler VJP's rebuilt MLP output feeds only the graph-only next_p: with
+# this set, install_v3's tiled MLP does not compute it (same gradients).
+SKIP_UNUSED_MLP_OUTPUT = True
+
 
 def _euler_inverse_for_vjp(block, p, q):
     """Invert one Euler step and rebuild its graph with one evaluation of
@@ -84,8 +90,11 @@ def _euler_inverse_for_vjp(block, p, q):
             q0 = euler_step(q, attention.detach(), -1)
         q0 = q0.detach().requires_grad_(True)
         next_q, normed = add_rms_norm(q0, attention, block.mlp_norm)
-        # next_p is only differentiated (its value is never read)
-        next_p = euler_step(p0_pass, block.mlp(normed), +1, graph_only=True)
+        # next_p is only differentiated (its value is never read), and so is
+        # the MLP output it adds: a tiled MLP skips its down projection
+        with output_unused() if SKIP_UNUSED_MLP_OUTPUT else contextlib.nullcontext():
+            force = block.mlp(normed)
+        next_p = euler_step(p0_pass, force, +1, graph_only=True)
     return next_p, next_q, p0, q0
 
 

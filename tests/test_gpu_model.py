@@ -373,6 +373,38 @@ def test_euler_attention_reuse_bitwise(cuda_device):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("keep_tiles", [False, True])
+def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles):
+    """The Euler VJP's rebuilt MLP output only feeds the graph-only next_p:
+    skipping its down projection leaves the loss and every gradient unchanged,
+    bit for bit."""
+    from reversability_amd import reversible
+    torch.manual_seed(13)
+    cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
+                     "d_model": 256, "d_ff": 512}, "method": "euler", "step_size": 0.5}
+    model = build_model(cfg).to(cuda_device)
+    install_v3(model, core_mode="reference", mlp_tokens=256, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=keep_tiles)
+    enable_linear(model)
+    enable_attention(model)
+    ids = torch.randint(0, 512, (2, 256), device=cuda_device)
+    runs = []
+    saved = reversible.SKIP_UNUSED_MLP_OUTPUT
+    try:
+        for skip in (False, True):
+            reversible.SKIP_UNUSED_MLP_OUTPUT = skip
+            model.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.float16):
+                loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+            loss.backward()
+            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
+    finally:
+        reversible.SKIP_UNUSED_MLP_OUTPUT = saved
+    assert torch.equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
+
+
 def test_split_midpoint_kept_attention_bitwise(cuda_device):
     """SplitMidpoint with the inversion's attention graph kept for the attention
     VJP gives the same loss and gradients, bit for bit, as recomputing it."""
