@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import threading
 
 import torch
 
@@ -51,28 +52,29 @@ def cast_f16(t: torch.Tensor) -> torch.Tensor:
 # Call-scoped cache of fp16 weight casts (see weight_cast_cache).
 _weight_cache: dict | None = None
 
-# Depth of output_unused blocks currently open.
-_output_unused = 0
+# Depth of the output_unused blocks open on each thread (autograd runs a CUDA
+# backward on its own device thread; another thread's forward is unaffected).
+_output_unused = threading.local()
 
 
 @contextlib.contextmanager
 def output_unused():
-    """Inside this block the tiled MLP's output is only differentiated, never
-    read: ``install_v3``'s MLP forward on a GPU tensor keeps its tiles for the
-    backward but skips the down projection (the output tensor is allocated,
-    not computed).  For an MLP evaluation that only feeds a rebuilt
-    ``graph_only`` residual step.  The backward is unchanged."""
-    global _output_unused
-    _output_unused += 1
+    """Inside this block (on this thread) the tiled MLP's output is only
+    differentiated, never read: ``install_v3``'s MLP forward on a GPU tensor
+    keeps its tiles for the backward but skips the down projection (the
+    output tensor is allocated, not computed).  For an MLP evaluation that
+    only feeds a rebuilt ``graph_only`` residual step.  The backward is
+    unchanged."""
+    _output_unused.depth = getattr(_output_unused, "depth", 0) + 1
     try:
         yield
     finally:
-        _output_unused -= 1
+        _output_unused.depth -= 1
 
 
 def output_wanted(x: torch.Tensor) -> bool:
-    """False inside ``output_unused`` for a GPU input."""
-    return not (_output_unused and x.is_cuda)
+    """False inside ``output_unused`` (on this thread) for a GPU input."""
+    return not (getattr(_output_unused, "depth", 0) and x.is_cuda)
 
 
 @contextlib.contextmanager

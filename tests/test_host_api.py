@@ -380,3 +380,24 @@ def test_weight_cast_cache_scope():
         assert len(calls) == 5          # the cache ends with the outer block
     finally:
         mlp.cast_f16 = original
+
+
+def test_mlp_output_unused_is_per_thread_and_gpu_only():
+    """mlp.output_unused() marks only the opening thread's GPU MLP calls (the
+    autograd device thread that runs a reconstruction backward); CPU inputs and
+    other threads always get their output computed."""
+    import threading
+    from reversability_amd import mlp
+    cpu = torch.zeros(2, 4)
+    meta_cuda = torch.empty(2, 4, device="meta")
+    assert mlp.output_wanted(cpu) and mlp.output_wanted(meta_cuda)
+    with mlp.output_unused():
+        with mlp.output_unused():
+            assert mlp.output_wanted(cpu)
+        other = []
+        worker = threading.Thread(target=lambda: other.append(getattr(mlp._output_unused,
+                                                                      "depth", 0)))
+        worker.start()
+        worker.join()
+        assert other == [0] and mlp._output_unused.depth == 1
+    assert mlp._output_unused.depth == 0
