@@ -188,6 +188,18 @@ int rv_rmsnorm_bwd_acc_pass(const float* x, const float* w, const void* dy, int 
                             void* dx16, float* dw, void* workspace, int64_t workspace_bytes,
                             int64_t rows, int64_t width, void* stream);
 
+/* The residual update's inverse fused into the norm that reads its result
+ * (the Euler inversion, reversible.py:28-32 with kernels_v3.py:9-16):
+ * d = x - f (f of dtype force_dtype: RV_F32 or RV_F16) and, with readd == 0,
+ * y = fp16(RMSNorm(d)), rstd; with readd != 0 also h = d + f and
+ * y = fp16(RMSNorm(h)) (the rebuilt step's sum).  The same values as
+ * rv_residual_axpy(x, f, -1) followed by rv_rmsnorm_fwd_f16 (or
+ * rv_add_rmsnorm_fwd_f16 of d and f), in one pass.  Vector path only:
+ * width % 4 == 0, x, w, d, h 16-byte aligned, y 8-byte aligned. */
+int rv_sub_rmsnorm_fwd_f16(const float* x, const void* f, int force_dtype, int readd,
+                           const float* w, float* d, float* h, void* y, float* rstd,
+                           int64_t rows, int64_t width, float eps, void* stream);
+
 /* Fused residual add + RMSNorm (the x + A(x) -> mlp_norm step of
  * midpoint_force and the q' = q + A(p) -> mlp_norm step of Euler):
  *   h[r, :] = x[r, :] + S(f[r, :])             (written to h)

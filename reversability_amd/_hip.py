@@ -71,6 +71,7 @@ SIGNATURES = {
     "rv_gemm_num_shapes": (_I, []),
     "rv_gemm_force_shape": (_I, [_I]),
     "rv_add_rmsnorm_fwd_f16": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
+    "rv_sub_rmsnorm_fwd_f16": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_rmsnorm_bwd_acc": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rv_rmsnorm_bwd_acc_pass": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                      _I64, _P]),
@@ -253,6 +254,27 @@ def _add_rmsnorm_fwd16(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: f
     return h, y, rstd
 
 
+def _sub_rmsnorm_fwd16(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: float,
+                       readd: bool):
+    """d = x - f and the fp16 RMSNorm of d (readd False) or of h = d + f
+    (readd True): (d, h (empty when not readd), y16, rstd)."""
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    d = torch.empty_like(x)
+    h = torch.empty_like(x) if readd else x.new_empty(0)
+    y = torch.empty_like(x, dtype=torch.float16)
+    rstd = torch.empty(rows, device=x.device, dtype=torch.float32)
+    if rows:
+        with _DeviceGuard(x):
+            _check(library().rv_sub_rmsnorm_fwd_f16(x.data_ptr(), f.data_ptr(), _dtype_code(f),
+                                                    int(readd), w.data_ptr(), d.data_ptr(),
+                                                    h.data_ptr() if readd else None,
+                                                    y.data_ptr(), rstd.data_ptr(), rows, width,
+                                                    eps, _stream(x)),
+                   "rv_sub_rmsnorm_fwd_f16")
+    return d, h, y, rstd
+
+
 def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.Tensor,
                      dh: Optional[torch.Tensor], f16: bool = True,
                      dpass: Optional[torch.Tensor] = None):
@@ -381,6 +403,8 @@ _SCHEMAS = {
                         _add_rmsnorm_fwd),
     "add_rmsnorm_fwd16": ("add_rmsnorm_fwd16(Tensor x, Tensor f, Tensor weight, float eps) "
                           "-> (Tensor, Tensor, Tensor)", _add_rmsnorm_fwd16),
+    "sub_rmsnorm_fwd16": ("sub_rmsnorm_fwd16(Tensor x, Tensor f, Tensor weight, float eps, "
+                          "bool readd) -> (Tensor, Tensor, Tensor, Tensor)", _sub_rmsnorm_fwd16),
     "rmsnorm_bwd_acc": ("rmsnorm_bwd_acc(Tensor x, Tensor weight, Tensor dy, Tensor rstd, "
                         "Tensor? dh, bool f16=True, Tensor? dpass=None) "
                         "-> (Tensor, Tensor, Tensor)",
@@ -426,6 +450,13 @@ def _(x, f, weight, eps):
 @torch.library.register_fake(f"{NAMESPACE}::add_rmsnorm_fwd16")
 def _(x, f, weight, eps):
     return (torch.empty_like(x), torch.empty_like(x, dtype=torch.float16),
+            x.new_empty(_fake_rows(x), dtype=torch.float32))
+
+
+@torch.library.register_fake(f"{NAMESPACE}::sub_rmsnorm_fwd16")
+def _(x, f, weight, eps, readd):
+    return (torch.empty_like(x), torch.empty_like(x) if readd else x.new_empty(0),
+            torch.empty_like(x, dtype=torch.float16),
             x.new_empty(_fake_rows(x), dtype=torch.float32))
 
 

@@ -114,11 +114,14 @@ __device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD>& t, const flo
   }
 }
 
-template <int VEC, int RPW, typename F, bool ADD, typename Y>
+// SUBM (with ADD): 0 -- the row input is x + f; 1 -- it is x - f; 2 -- d = x - f
+// is stored and the row input is d + f.
+template <int VEC, int RPW, typename F, bool ADD, typename Y, int SUBM = 0>
 __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const float4 (&wv)[VEC],
                                            float* __restrict__ h, Y* __restrict__ y,
                                            float* __restrict__ rstd, int64_t row0, int64_t rows,
-                                           int width, float eps, int lane) {
+                                           int width, float eps, int lane,
+                                           float* __restrict__ d = nullptr) {
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const int64_t row = row0 + r;
@@ -126,11 +129,23 @@ __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const f
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
       const bool ok = (v * 64 + lane) * 4 < width;
-      if constexpr (ADD) {
+      if constexpr (ADD && SUBM == 0) {
         t.x[r][v].x = t.x[r][v].x + t.f[r][v].x;
         t.x[r][v].y = t.x[r][v].y + t.f[r][v].y;
         t.x[r][v].z = t.x[r][v].z + t.f[r][v].z;
         t.x[r][v].w = t.x[r][v].w + t.f[r][v].w;
+      } else if constexpr (ADD) {
+        t.x[r][v].x = t.x[r][v].x - t.f[r][v].x;
+        t.x[r][v].y = t.x[r][v].y - t.f[r][v].y;
+        t.x[r][v].z = t.x[r][v].z - t.f[r][v].z;
+        t.x[r][v].w = t.x[r][v].w - t.f[r][v].w;
+        if constexpr (SUBM == 2) {
+          if (row < rows && ok) rv::st_f4s(d + row * width + (v * 64 + lane) * 4, t.x[r][v]);
+          t.x[r][v].x = t.x[r][v].x + t.f[r][v].x;
+          t.x[r][v].y = t.x[r][v].y + t.f[r][v].y;
+          t.x[r][v].z = t.x[r][v].z + t.f[r][v].z;
+          t.x[r][v].w = t.x[r][v].w + t.f[r][v].w;
+        }
       }
       const float4 q = rv::keep_if(t.x[r][v], ok);
       ss = ss + q.x * q.x;
@@ -160,12 +175,12 @@ __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const f
   }
 }
 
-template <int VEC, int RPW, typename F, bool ADD, typename Y>
+template <int VEC, int RPW, typename F, bool ADD, typename Y, int SUBM = 0>
 __global__ __launch_bounds__(kFwdWaves * 64)
 void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
                  const float* __restrict__ w, float* __restrict__ h,
                  Y* __restrict__ y, float* __restrict__ rstd,
-                 int64_t rows, int width, float eps) {
+                 int64_t rows, int width, float eps, float* __restrict__ d = nullptr) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * kFwdWaves;
   const int64_t wave = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
@@ -186,11 +201,11 @@ void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
   rms_load(a, x, f, row0, rows, width, lane);
   for (int64_t k = 0; k < iters; k += 2) {
     rms_load(b, x, f, row0 + stride, rows, width, lane);
-    rms_finish(a, wv, h, y, rstd, row0, rows, width, eps, lane);
+    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(a, wv, h, y, rstd, row0, rows, width, eps, lane, d);
     if (k + 1 >= iters) break;
     row0 += stride;
     rms_load(a, x, f, row0 + stride, rows, width, lane);
-    rms_finish(b, wv, h, y, rstd, row0, rows, width, eps, lane);
+    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(b, wv, h, y, rstd, row0, rows, width, eps, lane, d);
     row0 += stride;
   }
 }
@@ -584,6 +599,36 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, Y* y,
   }
 }
 
+// x - f (SUBM 1: stored in h, the norm's input) or d = x - f and h = d + f
+// (SUBM 2): vector path, fp16 y only.
+template <typename F, int SUBM>
+int launch_fwd_sub(const float* x, const F* f, const float* w, float* d, float* h, __half* y,
+                   float* rstd, int64_t rows, int width, float eps, hipStream_t stream) {
+  const bool vec = (width % 4 == 0) && rv_host::aligned16(x) && rv_host::aligned16(w) &&
+                   rv_host::aligned16(h) && (d == nullptr || rv_host::aligned16(d)) &&
+                   (reinterpret_cast<uintptr_t>(y) % 8) == 0 &&
+                   (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0;
+  if (!vec || width > 256 * kMaxVec) return RV_ERR_UNSUPPORTED;
+  constexpr int RPW = RV_RMS_FWD_RPW;
+  const int64_t rows_per_block = (int64_t)kFwdWaves * RPW;
+  int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+  const int64_t cap = (int64_t)rv_host::cu_count() * RV_RMS_FWD_BLOCKS_PER_CU;
+  if (blocks > cap) blocks = cap;
+  const dim3 grid((unsigned)blocks);
+  const dim3 block(kFwdWaves * 64);
+  const int vecs = (width + 255) / 256;
+#define RV_FWD_SUB(V)                                                                      \
+  hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, true, __half, SUBM>), grid, block, 0, stream, x, \
+                     f, w, h, y, rstd, rows, width, eps, d)
+  if (vecs <= 1) RV_FWD_SUB(1);
+  else if (vecs <= 2) RV_FWD_SUB(2);
+  else if (vecs <= 4) RV_FWD_SUB(4);
+  else if (vecs <= 8) RV_FWD_SUB(8);
+  else RV_FWD_SUB(16);
+#undef RV_FWD_SUB
+  return rv_host::check_launch();
+}
+
 template <typename G>
 int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, float* dx,
                float* dw, void* workspace, int64_t workspace_bytes, int64_t rows,
@@ -687,6 +732,30 @@ int rv_add_rmsnorm_fwd(const float* x, const void* f, int force_dtype,
       return launch_fwd<__hip_bfloat16, true>(x, (const __hip_bfloat16*)f, w,
                                               h, y, rstd, rows, (int)width,
                                               eps, s);
+    default:
+      return RV_ERR_UNSUPPORTED;
+  }
+}
+
+int rv_sub_rmsnorm_fwd_f16(const float* x, const void* f, int force_dtype, int readd,
+                           const float* w, float* d, float* h, void* y, float* rstd,
+                           int64_t rows, int64_t width, float eps, void* stream) {
+  if (!x || !f || !w || !d || !y || !rstd || (readd && !h)) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096) return RV_ERR_UNSUPPORTED;
+  const hipStream_t s = (hipStream_t)stream;
+  __half* y16 = static_cast<__half*>(y);
+  switch (force_dtype) {
+    case RV_F32:
+      return readd ? launch_fwd_sub<float, 2>(x, (const float*)f, w, d, h, y16, rstd, rows,
+                                              (int)width, eps, s)
+                   : launch_fwd_sub<float, 1>(x, (const float*)f, w, nullptr, d, y16, rstd,
+                                              rows, (int)width, eps, s);
+    case RV_F16:
+      return readd ? launch_fwd_sub<__half, 2>(x, (const __half*)f, w, d, h, y16, rstd, rows,
+                                               (int)width, eps, s)
+                   : launch_fwd_sub<__half, 1>(x, (const __half*)f, w, nullptr, d, y16, rstd,
+                                               rows, (int)width, eps, s);
     default:
       return RV_ERR_UNSUPPORTED;
   }

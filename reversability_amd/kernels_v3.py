@@ -74,9 +74,12 @@ class FusedAddRMSNorm(torch.autograd.Function):
     norm and autograd's accumulation and cast."""
 
     @staticmethod
-    def forward(ctx, x, f, weight, eps):
+    def forward(ctx, x, f, weight, eps, pre=None):
         ctx.set_materialize_grads(False)
-        h, y, rstd = ops.add_rmsnorm_fwd16(x, f, weight.contiguous(), float(eps))
+        if pre is None:
+            h, y, rstd = ops.add_rmsnorm_fwd16(x, f, weight.contiguous(), float(eps))
+        else:  # (h, y, rstd) already computed from these inputs (inverse_add_rms_norm)
+            h, y, rstd = pre
         ctx.save_for_backward(h, weight, rstd)
         ctx.f_dtype = f.dtype
         return h, y
@@ -92,7 +95,7 @@ class FusedAddRMSNorm(torch.autograd.Function):
         dx, dx16, dweight = ops.rmsnorm_bwd_acc(h, weight.contiguous(), dy.contiguous(), rstd,
                                                 dh.contiguous() if dh is not None else None)
         df = dx16 if ctx.f_dtype == torch.float16 else dx.to(ctx.f_dtype)
-        return dx, df, dweight, None
+        return dx, df, dweight, None, None
 
 
 class FusedRMSNormPass(torch.autograd.Function):
@@ -105,10 +108,13 @@ class FusedRMSNormPass(torch.autograd.Function):
     (fp16 under fp16 autocast with ``fp16_out``)."""
 
     @staticmethod
-    def forward(ctx, x, weight, eps, fp16_out=False):
+    def forward(ctx, x, weight, eps, fp16_out=False, pre=None):
         ctx.set_materialize_grads(False)
-        half = bool(fp16_out) and _fp16_out(x)
-        y, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps), half)
+        if pre is None:
+            half = bool(fp16_out) and _fp16_out(x)
+            y, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps), half)
+        else:  # (y, rstd) already computed from x (inverse_rms_norm)
+            y, rstd = pre
         ctx.save_for_backward(x, weight, rstd)
         return x.view_as(x), y
 
@@ -117,25 +123,63 @@ class FusedRMSNormPass(torch.autograd.Function):
     def backward(ctx, dpass, dy):
         x, weight, rstd = ctx.saved_tensors
         if dy is None:
-            return dpass, None, None, None
+            return dpass, None, None, None, None
         if dy.dtype not in (torch.float32, torch.float16):
             dy = dy.float()
         dx, _, dweight = ops.rmsnorm_bwd_acc(x, weight.contiguous(), dy.contiguous(), rstd,
                                              dpass.contiguous() if dpass is not None else None,
                                              False)
-        return dx, dweight, None, None
+        return dx, dweight, None, None, None
 
 
-def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module):
+def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module, pre=None):
     """``(x', norm(x))`` with x' = x for x's other use (see FusedRMSNormPass), on the
     fused kernels when ``norm`` is routed by ``enable_rmsnorm`` and x is a
     contiguous fp32 GPU tensor whose rows the vector kernels cover; otherwise
-    ``(x, norm(x))``."""
+    ``(x, norm(x))``.  ``pre``: the (y, rstd) ``inverse_rms_norm`` returned for x."""
     if (getattr(norm, "_rv_fused", False) and x.is_cuda and x.dtype == torch.float32
             and x.is_contiguous() and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0):
         return FusedRMSNormPass.apply(x, norm.weight, rms_norm_eps(norm, x),
-                                      getattr(norm, "_rv_fp16_out", False))
+                                      getattr(norm, "_rv_fp16_out", False), pre)
     return x, norm(x)
+
+
+def _sub_fusable(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module) -> bool:
+    """Whether rv_sub_rmsnorm_fwd_f16 gives what the fused fp16-output norm
+    paths (rms_norm_pass / add_rms_norm) would compute after ``x - f``."""
+    return (getattr(norm, "_rv_fused", False) and getattr(norm, "_rv_fp16_out", False)
+            and x.is_cuda and x.dtype == torch.float32
+            and f.dtype in (torch.float16, torch.float32) and x.shape == f.shape
+            and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
+            and _fp16_out(x))
+
+
+def inverse_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
+    """``(d, pre)`` with d = x - f (a residual step inverted, no graph) and
+    ``pre`` the (y, rstd) of ``norm(d)`` made in the same pass -- to hand to
+    ``rms_norm_pass(d, norm, pre)`` -- where the fused kernels apply; else
+    ``(euler_step(x, f, -1), None)``.  Same values either way."""
+    with torch.no_grad():
+        if _sub_fusable(x, f, norm):
+            d, _, y, rstd = ops.sub_rmsnorm_fwd16(x, f, norm.weight.contiguous(),
+                                                  rms_norm_eps(norm, x), False)
+            return d, (y, rstd)
+        from .residual import euler_step
+        return euler_step(x, f, -1), None
+
+
+def inverse_add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
+    """``(d, pre)`` with d = x - f (no graph) and ``pre`` the (h, y, rstd) of
+    ``add_rms_norm(d, f, norm)`` -- h = d + f and its norm -- made in the same
+    pass, to hand to ``add_rms_norm(d, f, norm, pre)``; else
+    ``(euler_step(x, f, -1), None)``.  Same values either way."""
+    with torch.no_grad():
+        if _sub_fusable(x, f, norm):
+            d, h, y, rstd = ops.sub_rmsnorm_fwd16(x, f, norm.weight.contiguous(),
+                                                  rms_norm_eps(norm, x), True)
+            return d, (h, y, rstd)
+        from .residual import euler_step
+        return euler_step(x, f, -1), None
 
 
 class FusedAddRMSNormPass(torch.autograd.Function):
@@ -181,16 +225,17 @@ def add_rms_norm_pass(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
     return x.view_as(x), add_rms_norm(x, f, norm)[1]
 
 
-def add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
+def add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module, pre=None):
     """``(h, norm(h))`` with ``h = x + f``.  On the fused kernels when ``norm``
     is an RMSNorm routed by ``enable_rmsnorm(..., fp16_out=True)`` and the
     call runs under fp16 autocast on the GPU; otherwise the residual add
-    (``residual.euler_step``) followed by ``norm``."""
+    (``residual.euler_step``) followed by ``norm``.  ``pre``: the (h, y, rstd)
+    ``inverse_add_rms_norm`` returned for these inputs."""
     if (getattr(norm, "_rv_fp16_out", False) and x.is_cuda and x.dtype == torch.float32
             and f.dtype in (torch.float16, torch.float32) and x.shape == f.shape
             and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
             and _fp16_out(x)):
-        return FusedAddRMSNorm.apply(x, f, norm.weight, rms_norm_eps(norm, x))
+        return FusedAddRMSNorm.apply(x, f, norm.weight, rms_norm_eps(norm, x), pre)
     from .residual import euler_step
     h = euler_step(x, f, +1)
     return h, norm(h)

@@ -25,7 +25,7 @@ import math
 import torch
 from torch.autograd.function import once_differentiable
 
-from .kernels_v3 import add_rms_norm, rms_norm_pass
+from .kernels_v3 import add_rms_norm, inverse_add_rms_norm, inverse_rms_norm, rms_norm_pass
 from .mlp import output_unused
 from .model import BaselineLM, Block, ModelConfig
 from .residual import euler_step, midpoint_step
@@ -67,6 +67,10 @@ def inverse_pair(block, p, q, method, h):
 # With this set the inversion keeps that evaluation's graph for the VJP.
 REUSE_EULER_ATTENTION = True
 
+# The Euler inversion's subtractions p - M(q) and q - A(p0) computed in the
+# passes of the norms that read their results (same values).
+FUSE_EULER_INVERSE = True
+
 # The Euler VJP's rebuilt MLP output feeds only the graph-only next_p: with
 # this set, install_v3's tiled MLP does not compute it (same gradients).
 SKIP_UNUSED_MLP_OUTPUT = True
@@ -79,17 +83,26 @@ def _euler_inverse_for_vjp(block, p, q):
     Returns (next_p, next_q, p0, q0) with p0, q0 the graph's leaves; next_p is
     for differentiation only (on the GPU its value is not computed)."""
     with torch.no_grad():
-        p0 = euler_step(p, block.mlp(block.mlp_norm(q)), -1)
+        force = block.mlp(block.mlp_norm(q))
+        if FUSE_EULER_INVERSE:  # p0 and attn_norm(p0) in one pass
+            p0, pre_p0 = inverse_rms_norm(p, force, block.attn_norm)
+        else:
+            p0, pre_p0 = euler_step(p, force, -1), None
+        del force
     with torch.enable_grad():
         p0 = p0.detach().requires_grad_(True)
         # p0 feeds attn_norm and next_p: its two gradients are summed in the
         # norm's backward pass (rms_norm_pass)
-        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm)
+        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0)
         attention = block.attn(normed_p0)
-        with torch.no_grad():
-            q0 = euler_step(q, attention.detach(), -1)
+        if FUSE_EULER_INVERSE:  # q0, q0 + A(p0) and its norm in one pass
+            q0, pre_q = inverse_add_rms_norm(q, attention.detach(), block.mlp_norm)
+        else:
+            with torch.no_grad():
+                q0 = euler_step(q, attention.detach(), -1)
+            pre_q = None
         q0 = q0.detach().requires_grad_(True)
-        next_q, normed = add_rms_norm(q0, attention, block.mlp_norm)
+        next_q, normed = add_rms_norm(q0, attention, block.mlp_norm, pre_q)
         # next_p is only differentiated (its value is never read), and so is
         # the MLP output it adds: a tiled MLP skips its down projection
         with output_unused() if SKIP_UNUSED_MLP_OUTPUT else contextlib.nullcontext():

@@ -291,6 +291,45 @@ def test_residual_axpy_bitwise(cuda_device, sign):
     assert np.array_equal(out.numpy(), oracle.euler(x.numpy(), f.numpy(), sign))
 
 
+@pytest.mark.parametrize("rows,width,f_dtype", [(1000, 256, torch.float16), (777, 1024, torch.float16),
+                                                (33, 1024, torch.float32), (5, 4096, torch.float16)])
+def test_sub_rmsnorm_matches_composition_bitwise(cuda_device, rows, width, f_dtype):
+    """rv_sub_rmsnorm_fwd_f16: d = x - f with the fp16 norm of d (readd off) or
+    of h = d + f (readd on) equals rv_residual_axpy(x, f, -1) followed by the
+    fp16 RMSNorm (or the fused add + norm of d and f), bit for bit."""
+    g = gen(31)
+    eps = float(torch.finfo(torch.float32).eps)
+    x = torch.randn(rows, width, generator=g).to(cuda_device)
+    f = torch.randn(rows, width, generator=g).to(f_dtype).to(cuda_device)
+    w = (1 + 0.02 * torch.randn(width, generator=g)).to(cuda_device)
+    d_ref = ops.residual_axpy(x, f, -1)
+    y_ref, rstd_ref = ops.rmsnorm_fwd(d_ref, w, eps, True)
+    d, h, y, rstd = ops.sub_rmsnorm_fwd16(x, f, w, eps, False)
+    assert h.numel() == 0
+    assert torch.equal(d, d_ref) and torch.equal(y, y_ref) and torch.equal(rstd, rstd_ref)
+    h_ref, y2_ref, rstd2_ref = ops.add_rmsnorm_fwd16(d_ref, f, w, eps)
+    d2, h2, y2, rstd2 = ops.sub_rmsnorm_fwd16(x, f, w, eps, True)
+    assert torch.equal(d2, d_ref) and torch.equal(h2, h_ref)
+    assert torch.equal(y2, y2_ref) and torch.equal(rstd2, rstd2_ref)
+
+
+def test_sub_rmsnorm_rejects(cuda_device):
+    lib = _hip.library()
+    x = torch.zeros(4, 6, device=cuda_device)
+    f = torch.zeros(4, 6, device=cuda_device, dtype=torch.float16)
+    w = torch.ones(6, device=cuda_device)
+    d, y, r = torch.empty_like(x), torch.empty_like(f), torch.empty(4, device=cuda_device)
+    stream = torch.cuda.current_stream().cuda_stream
+    # width 6 is not a multiple of 4: the vector-only entry point refuses it
+    assert lib.rv_sub_rmsnorm_fwd_f16(x.data_ptr(), f.data_ptr(), _hip.RV_F16, 0, w.data_ptr(),
+                                      d.data_ptr(), None, y.data_ptr(), r.data_ptr(), 4, 6,
+                                      1e-6, stream) == 3  # RV_ERR_UNSUPPORTED
+    # readd needs h
+    assert lib.rv_sub_rmsnorm_fwd_f16(x.data_ptr(), f.data_ptr(), _hip.RV_F16, 1, w.data_ptr(),
+                                      d.data_ptr(), None, y.data_ptr(), r.data_ptr(), 4, 6,
+                                      1e-6, stream) == 1  # RV_ERR_NULL_POINTER
+
+
 def test_empty_inputs_match_eager(cuda_device):
     """Zero rows through the autograd Functions: the same shapes and gradients
     as eager torch (dweight zero, no kernel launched)."""

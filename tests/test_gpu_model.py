@@ -373,11 +373,13 @@ def test_euler_attention_reuse_bitwise(cuda_device):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("switch", ["SKIP_UNUSED_MLP_OUTPUT", "FUSE_EULER_INVERSE"])
 @pytest.mark.parametrize("keep_tiles", [False, True])
-def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles):
-    """The Euler VJP's rebuilt MLP output only feeds the graph-only next_p:
-    skipping its down projection leaves the loss and every gradient unchanged,
-    bit for bit."""
+def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch):
+    """The Euler VJP's rebuilt MLP output only feeds the graph-only next_p
+    (SKIP_UNUSED_MLP_OUTPUT), and the inversion's subtractions can run inside
+    the norms that read them (FUSE_EULER_INVERSE): either switch leaves the
+    loss and every gradient unchanged, bit for bit."""
     from reversability_amd import reversible
     torch.manual_seed(13)
     cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
@@ -389,17 +391,17 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles):
     enable_attention(model)
     ids = torch.randint(0, 512, (2, 256), device=cuda_device)
     runs = []
-    saved = reversible.SKIP_UNUSED_MLP_OUTPUT
+    saved = getattr(reversible, switch)
     try:
-        for skip in (False, True):
-            reversible.SKIP_UNUSED_MLP_OUTPUT = skip
+        for on in (False, True):
+            setattr(reversible, switch, on)
             model.zero_grad(set_to_none=True)
             with torch.autocast("cuda", dtype=torch.float16):
                 loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
             loss.backward()
             runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
     finally:
-        reversible.SKIP_UNUSED_MLP_OUTPUT = saved
+        setattr(reversible, switch, saved)
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)
