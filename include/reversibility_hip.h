@@ -200,6 +200,19 @@ int rv_sub_rmsnorm_fwd_f16(const float* x, const void* f, int force_dtype, int r
                            const float* w, float* d, float* h, void* y, float* rstd,
                            int64_t rows, int64_t width, float eps, void* stream);
 
+/* The midpoint update fused into the norm that reads its result next (the
+ * next layer's attn_norm of next_q, reversible.py:21-25 / the reconstruction's
+ * prev_p, reversible.py:28-32, with kernels_v3.py:9-16): out = p +/- fp16(fp16(a
+ * + m) * scale) (sign +1 / -1; a, m fp16, the eager rounding points of
+ * rv_midpoint_update) and y = fp16(RMSNorm(out)), rstd -- the same values as
+ * rv_midpoint_update followed by rv_rmsnorm_fwd_f16, in one pass.  Vector
+ * path only: width % 4 == 0, p, w, out 16-byte aligned, a, m, y 8-byte
+ * aligned; force_dtype RV_F16. */
+int rv_midpoint_rmsnorm_fwd_f16(const float* p, const void* a, const void* m, int force_dtype,
+                                double scale, int sign, const float* w, float* out, void* y,
+                                float* rstd, int64_t rows, int64_t width, float eps,
+                                void* stream);
+
 /* Fused residual add + RMSNorm (the x + A(x) -> mlp_norm step of
  * midpoint_force and the q' = q + A(p) -> mlp_norm step of Euler):
  *   h[r, :] = x[r, :] + S(f[r, :])             (written to h)

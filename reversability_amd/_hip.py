@@ -72,6 +72,8 @@ SIGNATURES = {
     "rv_gemm_force_shape": (_I, [_I]),
     "rv_add_rmsnorm_fwd_f16": (_I, [_P, _P, _I, _P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_sub_rmsnorm_fwd_f16": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P, _I64, _I64, _F, _P]),
+    "rv_midpoint_rmsnorm_fwd_f16": (_I, [_P, _P, _P, _I, _D, _I, _P, _P, _P, _P, _I64, _I64, _F,
+                                         _P]),
     "rv_rmsnorm_bwd_acc": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rv_rmsnorm_bwd_acc_pass": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
                                      _I64, _P]),
@@ -275,6 +277,26 @@ def _sub_rmsnorm_fwd16(x: torch.Tensor, f: torch.Tensor, w: torch.Tensor, eps: f
     return d, h, y, rstd
 
 
+def _midpoint_rmsnorm_fwd16(p: torch.Tensor, a: torch.Tensor, m: torch.Tensor, w: torch.Tensor,
+                            eps: float, scale: float, sign: int):
+    """The midpoint update of p with fp16 a, m and the fp16 RMSNorm of the
+    result: (out, y16, rstd)."""
+    width = p.shape[-1]
+    rows = p.numel() // width if width else 0
+    out = torch.empty_like(p)
+    y = torch.empty_like(p, dtype=torch.float16)
+    rstd = torch.empty(rows, device=p.device, dtype=torch.float32)
+    if rows:
+        with _DeviceGuard(p):
+            _check(library().rv_midpoint_rmsnorm_fwd_f16(p.data_ptr(), a.data_ptr(), m.data_ptr(),
+                                                         _dtype_code(a), scale, sign,
+                                                         w.data_ptr(), out.data_ptr(),
+                                                         y.data_ptr(), rstd.data_ptr(), rows,
+                                                         width, eps, _stream(p)),
+                   "rv_midpoint_rmsnorm_fwd_f16")
+    return out, y, rstd
+
+
 def _rmsnorm_bwd_acc(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, rstd: torch.Tensor,
                      dh: Optional[torch.Tensor], f16: bool = True,
                      dpass: Optional[torch.Tensor] = None):
@@ -405,6 +427,9 @@ _SCHEMAS = {
                           "-> (Tensor, Tensor, Tensor)", _add_rmsnorm_fwd16),
     "sub_rmsnorm_fwd16": ("sub_rmsnorm_fwd16(Tensor x, Tensor f, Tensor weight, float eps, "
                           "bool readd) -> (Tensor, Tensor, Tensor, Tensor)", _sub_rmsnorm_fwd16),
+    "midpoint_rmsnorm_fwd16": ("midpoint_rmsnorm_fwd16(Tensor p, Tensor a, Tensor m, "
+                               "Tensor weight, float eps, float scale, int sign) "
+                               "-> (Tensor, Tensor, Tensor)", _midpoint_rmsnorm_fwd16),
     "rmsnorm_bwd_acc": ("rmsnorm_bwd_acc(Tensor x, Tensor weight, Tensor dy, Tensor rstd, "
                         "Tensor? dh, bool f16=True, Tensor? dpass=None) "
                         "-> (Tensor, Tensor, Tensor)",
@@ -458,6 +483,12 @@ def _(x, f, weight, eps, readd):
     return (torch.empty_like(x), torch.empty_like(x) if readd else x.new_empty(0),
             torch.empty_like(x, dtype=torch.float16),
             x.new_empty(_fake_rows(x), dtype=torch.float32))
+
+
+@torch.library.register_fake(f"{NAMESPACE}::midpoint_rmsnorm_fwd16")
+def _(p, a, m, weight, eps, scale, sign):
+    return (torch.empty_like(p), torch.empty_like(p, dtype=torch.float16),
+            p.new_empty(_fake_rows(p), dtype=torch.float32))
 
 
 @torch.library.register_fake(f"{NAMESPACE}::rmsnorm_bwd_acc")

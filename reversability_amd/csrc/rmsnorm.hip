@@ -91,16 +91,19 @@ __device__ __forceinline__ void store_y(__half* p, float4 v) {
   __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(p));
 }
 
-template <int VEC, int RPW, typename F, bool ADD>
+// TWO: a second force operand g (the midpoint update's M(...) beside f = A(...)).
+template <int VEC, int RPW, typename F, bool ADD, bool TWO = false>
 struct RowTile {
   float4 x[RPW][VEC];
   float4 f[ADD ? RPW : 1][VEC];
+  float4 g[TWO ? RPW : 1][TWO ? VEC : 1];
 };
 
-template <int VEC, int RPW, typename F, bool ADD>
-__device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD>& t, const float* __restrict__ x,
-                                         const F* __restrict__ f, int64_t row0, int64_t rows,
-                                         int width, int lane) {
+template <int VEC, int RPW, typename F, bool ADD, bool TWO>
+__device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD, TWO>& t,
+                                         const float* __restrict__ x, const F* __restrict__ f,
+                                         int64_t row0, int64_t rows, int width, int lane,
+                                         const F* __restrict__ g = nullptr) {
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
@@ -110,18 +113,35 @@ __device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD>& t, const flo
       const int col_c = col < width ? col : width - 4;
       t.x[r][v] = rv::ld_f4(x + row * width + col_c);
       if constexpr (ADD) t.f[r][v] = rv::load4f(f + row * width + col_c);
+      if constexpr (TWO) t.g[r][v] = rv::load4f(g + row * width + col_c);
     }
   }
 }
 
+// The midpoint update of one element with the eager expression's rounding
+// points (fp16 force): c = fp16(fp16(a + m) * scale), x +/- c.  The empty asm
+// keeps the fp32 product from being folded into a mixed-precision FMA that
+// would round the exact product to fp16 once.
+__device__ __forceinline__ float midpoint_elem(float x, float a, float m, float scale, int sign) {
+  const float fsum = __half2float(__float2half_rn(a + m));
+  float prod = fsum * scale;
+  asm volatile("" : "+v"(prod));
+  const float c = __half2float(__float2half_rn(prod));
+  return sign > 0 ? x + c : x - c;
+}
+
 // SUBM (with ADD): 0 -- the row input is x + f; 1 -- it is x - f; 2 -- d = x - f
-// is stored and the row input is d + f.
+// is stored and the row input is d + f; 3 -- it is the midpoint update of x
+// with the force terms f and g (midpoint_elem).  The row input is stored in h
+// for every SUBM but 0 without h.
 template <int VEC, int RPW, typename F, bool ADD, typename Y, int SUBM = 0>
-__device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const float4 (&wv)[VEC],
+__device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD, SUBM == 3>& t,
+                                           const float4 (&wv)[VEC],
                                            float* __restrict__ h, Y* __restrict__ y,
                                            float* __restrict__ rstd, int64_t row0, int64_t rows,
                                            int width, float eps, int lane,
-                                           float* __restrict__ d = nullptr) {
+                                           float* __restrict__ d = nullptr, float scale = 0.f,
+                                           int sign = 1) {
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const int64_t row = row0 + r;
@@ -134,6 +154,11 @@ __device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD>& t, const f
         t.x[r][v].y = t.x[r][v].y + t.f[r][v].y;
         t.x[r][v].z = t.x[r][v].z + t.f[r][v].z;
         t.x[r][v].w = t.x[r][v].w + t.f[r][v].w;
+      } else if constexpr (ADD && SUBM == 3) {
+        t.x[r][v].x = midpoint_elem(t.x[r][v].x, t.f[r][v].x, t.g[r][v].x, scale, sign);
+        t.x[r][v].y = midpoint_elem(t.x[r][v].y, t.f[r][v].y, t.g[r][v].y, scale, sign);
+        t.x[r][v].z = midpoint_elem(t.x[r][v].z, t.f[r][v].z, t.g[r][v].z, scale, sign);
+        t.x[r][v].w = midpoint_elem(t.x[r][v].w, t.f[r][v].w, t.g[r][v].w, scale, sign);
       } else if constexpr (ADD) {
         t.x[r][v].x = t.x[r][v].x - t.f[r][v].x;
         t.x[r][v].y = t.x[r][v].y - t.f[r][v].y;
@@ -180,7 +205,8 @@ __global__ __launch_bounds__(kFwdWaves * 64)
 void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
                  const float* __restrict__ w, float* __restrict__ h,
                  Y* __restrict__ y, float* __restrict__ rstd,
-                 int64_t rows, int width, float eps, float* __restrict__ d = nullptr) {
+                 int64_t rows, int width, float eps, float* __restrict__ d = nullptr,
+                 const F* __restrict__ g = nullptr, float scale = 0.f, int sign = 1) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * kFwdWaves;
   const int64_t wave = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
@@ -197,15 +223,17 @@ void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
   }
   const int64_t stride = nwaves * RPW;
   int64_t row0 = wave * RPW;
-  RowTile<VEC, RPW, F, ADD> a, b;
-  rms_load(a, x, f, row0, rows, width, lane);
+  RowTile<VEC, RPW, F, ADD, SUBM == 3> a, b;
+  rms_load(a, x, f, row0, rows, width, lane, g);
   for (int64_t k = 0; k < iters; k += 2) {
-    rms_load(b, x, f, row0 + stride, rows, width, lane);
-    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(a, wv, h, y, rstd, row0, rows, width, eps, lane, d);
+    rms_load(b, x, f, row0 + stride, rows, width, lane, g);
+    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(a, wv, h, y, rstd, row0, rows, width, eps, lane, d,
+                                          scale, sign);
     if (k + 1 >= iters) break;
     row0 += stride;
-    rms_load(a, x, f, row0 + stride, rows, width, lane);
-    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(b, wv, h, y, rstd, row0, rows, width, eps, lane, d);
+    rms_load(a, x, f, row0 + stride, rows, width, lane, g);
+    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(b, wv, h, y, rstd, row0, rows, width, eps, lane, d,
+                                          scale, sign);
     row0 += stride;
   }
 }
@@ -599,15 +627,18 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, Y* y,
   }
 }
 
-// x - f (SUBM 1: stored in h, the norm's input) or d = x - f and h = d + f
-// (SUBM 2): vector path, fp16 y only.
+// x - f (SUBM 1: stored in h, the norm's input), d = x - f and h = d + f
+// (SUBM 2), or the midpoint update of x with f and g (SUBM 3, stored in h):
+// vector path, fp16 y only.
 template <typename F, int SUBM>
 int launch_fwd_sub(const float* x, const F* f, const float* w, float* d, float* h, __half* y,
-                   float* rstd, int64_t rows, int width, float eps, hipStream_t stream) {
+                   float* rstd, int64_t rows, int width, float eps, hipStream_t stream,
+                   const F* g = nullptr, float scale = 0.f, int sign = 1) {
   const bool vec = (width % 4 == 0) && rv_host::aligned16(x) && rv_host::aligned16(w) &&
                    rv_host::aligned16(h) && (d == nullptr || rv_host::aligned16(d)) &&
                    (reinterpret_cast<uintptr_t>(y) % 8) == 0 &&
-                   (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0;
+                   (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0 &&
+                   (reinterpret_cast<uintptr_t>(g) % (4 * sizeof(F))) == 0;
   if (!vec || width > 256 * kMaxVec) return RV_ERR_UNSUPPORTED;
   constexpr int RPW = RV_RMS_FWD_RPW;
   const int64_t rows_per_block = (int64_t)kFwdWaves * RPW;
@@ -619,7 +650,7 @@ int launch_fwd_sub(const float* x, const F* f, const float* w, float* d, float* 
   const int vecs = (width + 255) / 256;
 #define RV_FWD_SUB(V)                                                                      \
   hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, true, __half, SUBM>), grid, block, 0, stream, x, \
-                     f, w, h, y, rstd, rows, width, eps, d)
+                     f, w, h, y, rstd, rows, width, eps, d, g, scale, sign)
   if (vecs <= 1) RV_FWD_SUB(1);
   else if (vecs <= 2) RV_FWD_SUB(2);
   else if (vecs <= 4) RV_FWD_SUB(4);
@@ -759,6 +790,19 @@ int rv_sub_rmsnorm_fwd_f16(const float* x, const void* f, int force_dtype, int r
     default:
       return RV_ERR_UNSUPPORTED;
   }
+}
+
+int rv_midpoint_rmsnorm_fwd_f16(const float* p, const void* a, const void* m, int force_dtype,
+                                double scale, int sign, const float* w, float* out, void* y,
+                                float* rstd, int64_t rows, int64_t width, float eps,
+                                void* stream) {
+  if (!p || !a || !m || !w || !out || !y || !rstd) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > 4096 || force_dtype != RV_F16) return RV_ERR_UNSUPPORTED;
+  return launch_fwd_sub<__half, 3>(p, static_cast<const __half*>(a), w, nullptr, out,
+                                   static_cast<__half*>(y), rstd, rows, (int)width, eps,
+                                   (hipStream_t)stream, static_cast<const __half*>(m),
+                                   (float)scale, sign);
 }
 
 int64_t rv_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t width) {

@@ -168,6 +168,25 @@ def inverse_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
         return euler_step(x, f, -1), None
 
 
+def midpoint_rms_norm(p: torch.Tensor, a: torch.Tensor, m: torch.Tensor, scale: float,
+                      sign: int, norm: torch.nn.Module):
+    """``(out, pre)`` with out = ``residual.midpoint_step(p, a, m, scale, sign)``
+    (no graph) and ``pre`` the (y, rstd) of ``norm(out)`` made in the same pass
+    -- the value the next layer's attention norm reads, to use directly or hand
+    to ``rms_norm_pass(out, norm, pre)`` -- where the fused kernels apply (fp16
+    force terms); else ``(midpoint_step(...), None)``.  Same values either way."""
+    with torch.no_grad():
+        if (_sub_fusable(p, a, norm) and a.dtype == torch.float16
+                and m.dtype == torch.float16 and m.shape == p.shape and m.is_contiguous()
+                and m.data_ptr() % 16 == 0):
+            out, y, rstd = ops.midpoint_rmsnorm_fwd16(p, a, m, norm.weight.contiguous(),
+                                                      rms_norm_eps(norm, p), float(scale),
+                                                      int(sign))
+            return out, (y, rstd)
+        from .residual import midpoint_step
+        return midpoint_step(p, a, m, scale, sign), None
+
+
 def inverse_add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
     """``(d, pre)`` with d = x - f (no graph) and ``pre`` the (h, y, rstd) of
     ``add_rms_norm(d, f, norm)`` -- h = d + f and its norm -- made in the same

@@ -25,7 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
-from .kernels_v3 import add_rms_norm, add_rms_norm_pass, rms_norm_pass
+from .kernels_v3 import add_rms_norm, add_rms_norm_pass, midpoint_rms_norm, rms_norm_pass
 from .optimized import ReusedMidpoint, amp_context, hidden_states
 from .residual import midpoint_step
 
@@ -197,6 +197,11 @@ class TiledMLP(torch.autograd.Function):
 KEEP_SPLIT_ATTENTION = True
 
 
+# Each midpoint update made together with the attention norm of the layer that
+# reads it next (forward and reconstruction; same values).
+FUSE_MIDPOINT_NORM = True
+
+
 class SplitMidpoint(torch.autograd.Function):
     """MLP VJP first, then the attention VJP (optimized_v3.py:66-117).
 
@@ -212,9 +217,22 @@ class SplitMidpoint(torch.autograd.Function):
         ctx.device = p.device.type
         ctx.amp = torch.is_autocast_enabled(ctx.device)
         ctx.dtype = torch.get_autocast_dtype(ctx.device)
-        from .reversible import forward_pair
-        for block in blocks:
-            p, q = forward_pair(block, p, q, "midpoint", h)
+        from .reversible import midpoint_terms
+        normed = None  # the next block's attn_norm(q), made with the midpoint update
+        for i, block in enumerate(blocks):
+            if normed is None:
+                attention, mlp = midpoint_terms(block, q)
+            else:
+                attention = block.attn(normed)
+                mlp = block.mlp(add_rms_norm(q, attention, block.mlp_norm)[1])
+            lower = blocks[i + 1] if i + 1 < len(blocks) else None
+            if FUSE_MIDPOINT_NORM and lower is not None:
+                nxt, pre = midpoint_rms_norm(p, attention, mlp, 2 * h, +1, lower.attn_norm)
+                normed = pre[0] if pre is not None else None
+            else:
+                nxt, normed = midpoint_step(p, attention, mlp, 2 * h, +1), None
+            p, q = q, nxt
+            del attention, mlp
         ctx.save_for_backward(p, q, *parameters)
         return p, q
 
@@ -228,11 +246,14 @@ class SplitMidpoint(torch.autograd.Function):
         # otherwise leave history-free fp16 weight casts for the grad-enabled
         # rebuild (torch <= 2.10); casts are deterministic, values unchanged.
         with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype, cache_enabled=False):
-            for block in reversed(ctx.blocks):
+            pre_p = None  # attn_norm(p) of this block, made with the previous inversion
+            for index in reversed(range(len(ctx.blocks))):
+                block = ctx.blocks[index]
+                lower = ctx.blocks[index - 1] if index > 0 else None
                 if KEEP_SPLIT_ATTENTION:  # its graph serves the attention VJP below
                     with torch.enable_grad():
                         attn_input = p.detach().requires_grad_(True)
-                        attn_pass, normed = rms_norm_pass(attn_input, block.attn_norm)
+                        attn_pass, normed = rms_norm_pass(attn_input, block.attn_norm, pre_p)
                         attention = block.attn(normed)
                 else:
                     with torch.no_grad():
@@ -244,8 +265,15 @@ class SplitMidpoint(torch.autograd.Function):
                     # gradients are summed in the norm's backward pass
                     q_pass, mlp_in = add_rms_norm_pass(previous_q, proxy, block.mlp_norm)
                     mlp = block.mlp(mlp_in)
-                    with torch.no_grad():
-                        previous_p = midpoint_step(q, proxy.detach(), mlp.detach(), scale, -1)
+                    if FUSE_MIDPOINT_NORM and KEEP_SPLIT_ATTENTION and lower is not None:
+                        # previous_p with the lower block's attn_norm of it
+                        previous_p, pre_p = midpoint_rms_norm(q, proxy.detach(), mlp.detach(),
+                                                              scale, -1, lower.attn_norm)
+                    else:
+                        with torch.no_grad():
+                            previous_p = midpoint_step(q, proxy.detach(), mlp.detach(), scale,
+                                                       -1)
+                        pre_p = None
                     previous_p.requires_grad_(True)
                     # only differentiated: its value is never read
                     next_q = midpoint_step(previous_p, proxy, mlp, scale, +1, graph_only=True)

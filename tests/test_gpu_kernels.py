@@ -313,6 +313,23 @@ def test_sub_rmsnorm_matches_composition_bitwise(cuda_device, rows, width, f_dty
     assert torch.equal(y2, y2_ref) and torch.equal(rstd2, rstd2_ref)
 
 
+@pytest.mark.parametrize("rows,width,scale,sign", [(1000, 256, 1.0, 1), (777, 1024, 0.5, -1),
+                                                   (33, 256, 0.3, -1), (5, 4096, 0.5, 1)])
+def test_midpoint_rmsnorm_matches_composition_bitwise(cuda_device, rows, width, scale, sign):
+    """rv_midpoint_rmsnorm_fwd_f16 equals rv_midpoint_update followed by the
+    fp16 RMSNorm of its result, bit for bit."""
+    g = gen(37)
+    eps = float(torch.finfo(torch.float32).eps)
+    p = torch.randn(rows, width, generator=g).to(cuda_device)
+    a = torch.randn(rows, width, generator=g).half().to(cuda_device)
+    m = torch.randn(rows, width, generator=g).half().to(cuda_device)
+    w = (1 + 0.02 * torch.randn(width, generator=g)).to(cuda_device)
+    out_ref = ops.midpoint_update(p, a, m, scale, sign)
+    y_ref, rstd_ref = ops.rmsnorm_fwd(out_ref, w, eps, True)
+    out, y, rstd = ops.midpoint_rmsnorm_fwd16(p, a, m, w, eps, scale, sign)
+    assert torch.equal(out, out_ref) and torch.equal(y, y_ref) and torch.equal(rstd, rstd_ref)
+
+
 def test_sub_rmsnorm_rejects(cuda_device):
     lib = _hip.library()
     x = torch.zeros(4, 6, device=cuda_device)

@@ -407,6 +407,37 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch
         assert torch.equal(a, b)
 
 
+def test_split_midpoint_fused_update_norm_bitwise(cuda_device):
+    """The split midpoint core with each midpoint update made together with
+    the next layer's attention norm (FUSE_MIDPOINT_NORM) gives the same loss
+    and gradients, bit for bit, as the separate update and norm."""
+    from reversability_amd import optimized_v3
+    torch.manual_seed(17)
+    cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
+                     "d_model": 256, "d_ff": 512}, "method": "midpoint", "step_size": 0.5}
+    model = build_model(cfg).to(cuda_device)
+    install_v3(model, core_mode="split", mlp_tokens=512, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
+    enable_linear(model)
+    enable_attention(model)
+    ids = torch.randint(0, 512, (2, 256), device=cuda_device)
+    runs = []
+    saved = optimized_v3.FUSE_MIDPOINT_NORM
+    try:
+        for on in (False, True):
+            optimized_v3.FUSE_MIDPOINT_NORM = on
+            model.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.float16):
+                loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+            loss.backward()
+            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
+    finally:
+        optimized_v3.FUSE_MIDPOINT_NORM = saved
+    assert torch.equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
+
+
 def test_split_midpoint_kept_attention_bitwise(cuda_device):
     """SplitMidpoint with the inversion's attention graph kept for the attention
     VJP gives the same loss and gradients, bit for bit, as recomputing it."""
