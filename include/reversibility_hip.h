@@ -86,6 +86,21 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
                    int64_t workspace_bytes, int64_t rows, int64_t width,
                    void* stream);
 
+/* rv_rmsnorm_bwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: it is
+ * rv_rmsnorm_bwd's computation (the same kernels, bit-identical dx and dw)
+ * with the dweight partial sums kept in a static device array of 4 MiB
+ * (256 x 4096 fp32) that each GPU holds from the first call on that device
+ * until the process ends.  The call allocates nothing (no hipMalloc / hipFree,
+ * no library allocation); its first call on a device looks up the array's
+ * address there.  width <= 4096 (RV_ERR_UNSUPPORTED otherwise).  All calls on
+ * one GPU share the array: calls that overlap on one GPU (concurrent streams,
+ * threads) race and must be ordered by the caller. */
+int rv_rmsnorm_bwd_noalloc(const float* x, const float* w, const float* dy,
+                           const float* rstd, float* dx, float* dw,
+                           int64_t rows, int64_t width, void* stream);
+
 /* ------------------------------------------------------------------------
  * SwiGLU over a packed up-projection u[rows, ld_u]: gate = u[:, 0:width],
  * value = u[:, width:2*width].  dtype is RV_F16 or RV_F32.

@@ -43,6 +43,7 @@ SIGNATURES = {
     "rv_rmsnorm_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_rmsnorm_bwd_workspace_bytes": (_I64, [_I64, _I64]),
     "rv_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
+    "rv_rmsnorm_bwd_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P]),
     "rv_rmsnorm_fwd_f16": (_I, [_P, _P, _P, _P, _I64, _I64, _F, _P]),
     "rv_rmsnorm_bwd_f16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "rv_swiglu_fwd": (_I, [_P, _I64, _P, _I64, _I64, _I, _P]),

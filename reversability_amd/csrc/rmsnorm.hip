@@ -24,6 +24,7 @@
 // forward multiply order x*r inside the dweight sum); the build disables FMA
 // contraction to match the reference's enable_fp_fusion=False.
 
+#include <mutex>
 #include <type_traits>
 
 #include "rv_device.h"
@@ -732,6 +733,47 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
   return rv_host::check_launch();
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the backward entry point that allocates nothing
+// (rv_rmsnorm_bwd_noalloc): the dweight partial rows, at most
+// kBwdTargetBlocks x 4096 fp32 (4 MiB).  Every GPU the library runs on holds
+// its own copy of this array until the process ends.  Host code never passes
+// the array's name to a kernel (on the host it is only a stand-in for the
+// symbol): the device address comes from hipGetSymbolAddress, queried once
+// per device with that device current, and is cached per device.
+// ---------------------------------------------------------------------------
+constexpr int kNoallocMaxWidth = 4096;
+constexpr int64_t kNoallocScratchFloats = kBwdTargetBlocks * kNoallocMaxWidth;
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, per device
+
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoallocScratchFloats];
+
+namespace {
+
+// The current device's address of `scratch` (queried on its first use on that
+// device), or an rv_status.
+int scratch_address(float** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return rv_host::hip_fail(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return RV_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return rv_host::hip_fail(err);
+    if (ptr == nullptr) return RV_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<float*>(g_scratch_ptr[dev]);
+  return RV_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -817,6 +859,22 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
                    void* stream) {
   return launch_bwd<float>(x, w, dy, rstd, dx, dw, workspace, workspace_bytes, rows, width,
                            (hipStream_t)stream);
+}
+
+int rv_rmsnorm_bwd_noalloc(const float* x, const float* w, const float* dy, const float* rstd,
+                           float* dx, float* dw, int64_t rows, int64_t width, void* stream) {
+  // Argument checks first: a rejected call touches no device state.
+  if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
+  if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
+  if (width > kNoallocMaxWidth) return RV_ERR_UNSUPPORTED;
+  const int64_t need = (int64_t)plan_bwd(rows).nparts * width * (int64_t)sizeof(float);
+  if (need > kNoallocScratchFloats * (int64_t)sizeof(float)) return RV_ERR_WORKSPACE;
+  float* ws = nullptr;
+  const int st = scratch_address(&ws);
+  if (st != RV_OK) return st;
+  // The partial rows are written in full before the reduce reads them, so the
+  // previous call's contents need no clearing.
+  return launch_bwd<float>(x, w, dy, rstd, dx, dw, ws, need, rows, width, (hipStream_t)stream);
 }
 
 int rv_rmsnorm_fwd_f16(const float* x, const float* w, void* y, float* rstd, int64_t rows,

@@ -1,0 +1,81 @@
+"""rv_rmsnorm_bwd_noalloc (the RMSNorm backward that allocates nothing, its
+dweight partials in a static device array) against rv_rmsnorm_bwd (caller
+workspace), through the C ABI: bit-identical dx and dw on two calls in a row,
+the second with a smaller input, so the second call runs over the first
+call's leftover scratch contents."""
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from reversability_amd import _hip
+
+EPS = float(torch.finfo(torch.float32).eps)
+
+
+def _inputs(rows, width, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, width, generator=g)
+    w = 1 + 0.02 * torch.randn(width, generator=g)
+    dy = torch.randn(rows, width, generator=g)
+    x, w, dy = x.to(dev), w.to(dev), dy.to(dev)
+    _, rstd = _hip.ops.rmsnorm_fwd(x, w, EPS)
+    return x, w, dy, rstd
+
+
+def _with_workspace(lib, x, w, dy, rstd):
+    rows, width = x.shape
+    dx, dw = torch.empty_like(x), torch.empty_like(w)
+    nbytes = lib.rv_rmsnorm_bwd_workspace_bytes(rows, width)
+    ws = torch.empty(nbytes // 4, device=x.device)
+    st = lib.rv_rmsnorm_bwd(x.data_ptr(), w.data_ptr(), dy.data_ptr(), rstd.data_ptr(),
+                            dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), nbytes, rows, width,
+                            _hip._stream(x))
+    assert st == 0, lib.rv_status_string(st)
+    return dx, dw
+
+
+def _noalloc(lib, x, w, dy, rstd):
+    rows, width = x.shape
+    dx = torch.full_like(x, float("nan"))
+    dw = torch.full_like(w, float("nan"))
+    st = lib.rv_rmsnorm_bwd_noalloc(x.data_ptr(), w.data_ptr(), dy.data_ptr(), rstd.data_ptr(),
+                                    dx.data_ptr(), dw.data_ptr(), rows, width, _hip._stream(x))
+    assert st == 0, lib.rv_status_string(st)
+    return dx, dw
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shapes", [
+    ((14848, 256), (1000, 256)),    # configs[0], then fewer rows
+    ((32768, 1024), (4099, 1020)),  # configs[4]'s norm width, then a narrower ragged one
+    ((300, 4096), (7, 66)),         # the maximum width, then the scalar path
+])
+def test_noalloc_matches_workspace_entry_point(cuda_device, shapes):
+    lib = _hip.library()
+    for i, (rows, width) in enumerate(shapes):
+        print(f"[noalloc] call {i}: rows={rows} width={width}", flush=True)
+        x, w, dy, rstd = _inputs(rows, width, 1337 + i, cuda_device)
+        ref_dx, ref_dw = _with_workspace(lib, x, w, dy, rstd)
+        dx, dw = _noalloc(lib, x, w, dy, rstd)
+        torch.cuda.synchronize()
+        assert torch.equal(dx, ref_dx), (rows, width)
+        assert torch.equal(dw, ref_dw), (rows, width)
+
+
+@pytest.mark.gpu
+def test_noalloc_rejects_sizes_beyond_its_scratch(cuda_device):
+    lib = _hip.library()
+    x = torch.zeros(4, 8192, device=cuda_device)
+    w = torch.ones(8192, device=cuda_device)
+    rstd = torch.ones(4, device=cuda_device)
+    st = lib.rv_rmsnorm_bwd_noalloc(x.data_ptr(), w.data_ptr(), x.data_ptr(), rstd.data_ptr(),
+                                    x.data_ptr(), w.data_ptr(), 4, 8192, _hip._stream(x))
+    assert st == 3  # RV_ERR_UNSUPPORTED: width above the 4096 the scratch is sized for
+    assert lib.rv_rmsnorm_bwd_noalloc(None, w.data_ptr(), x.data_ptr(), rstd.data_ptr(),
+                                      x.data_ptr(), w.data_ptr(), 4, 256, None) == 1
+    assert lib.rv_rmsnorm_bwd_noalloc(ctypes.c_void_p(x.data_ptr()), w.data_ptr(), x.data_ptr(),
+                                      rstd.data_ptr(), x.data_ptr(), w.data_ptr(), 0, 256,
+                                      None) == 2
