@@ -14,7 +14,8 @@ query; backward is deterministic (no atomics).
 ``enable_attention(model)`` patches every block's ``attn.forward``; calls the
 kernels do not cover (no fp16 ``qkv`` -- i.e. not under fp16 autocast --, head
 sizes other than 32/64/128, dropout in training mode, CPU tensors) keep the
-reference computation.
+reference computation, recorded in ``paths.report()`` (or raising under
+``paths.strict()``).
 """
 from __future__ import annotations
 
@@ -24,6 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
+from . import paths
 from ._hip import _check, _stream, library
 
 HEAD_DIMS = (32, 64, 128)
@@ -95,8 +97,13 @@ def enable_attention(model: torch.nn.Module) -> None:
         qkv = attn.qkv(x)
         dropout = attn.dropout if attn.training else 0.0
         if supported(qkv, attn.n_heads, dropout):
+            paths.took("attention", "hip")
             mixed = CausalAttention.apply(qkv, attn.n_heads)
         else:
+            paths.took("attention", "sdpa",
+                       f"attention kernels need a CUDA fp16 qkv, head size in {HEAD_DIMS} and no "
+                       f"dropout (got {qkv.dtype} on {qkv.device.type}, head size "
+                       f"{qkv.shape[-1] // (3 * attn.n_heads)}, dropout {dropout})")
             mixed = reference_attention(qkv, attn.n_heads, dropout)
         return attn.proj(mixed)
     for block in model.blocks:

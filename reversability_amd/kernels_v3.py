@@ -29,10 +29,12 @@ def _validate(x: torch.Tensor, weight: torch.Tensor) -> None:
         raise ValueError("Contiguous input and one-dimensional matching norm weight required")
 
 
-def _fp16_out(x: torch.Tensor) -> bool:
-    """fp16 output applies under fp16 autocast on rows the vector kernels cover."""
+def _fp16_out(x: torch.Tensor, weight: torch.Tensor | None = None) -> bool:
+    """fp16 output applies under fp16 autocast on rows the vector kernels cover
+    (16-byte aligned rows, and a contiguous, 16-byte aligned weight)."""
     return (torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.float16
-            and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0)
+            and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0
+            and (weight is None or (weight.is_contiguous() and weight.data_ptr() % 16 == 0)))
 
 
 class FusedRMSNorm(torch.autograd.Function):
@@ -47,7 +49,7 @@ class FusedRMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, eps, fp16_out=False):
         _validate(x, weight)
-        half = bool(fp16_out) and _fp16_out(x)
+        half = bool(fp16_out) and _fp16_out(x, weight)
         output, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps), half)
         ctx.save_for_backward(x, weight, rstd)
         return output
@@ -111,7 +113,7 @@ class FusedRMSNormPass(torch.autograd.Function):
     def forward(ctx, x, weight, eps, fp16_out=False, pre=None):
         ctx.set_materialize_grads(False)
         if pre is None:
-            half = bool(fp16_out) and _fp16_out(x)
+            half = bool(fp16_out) and _fp16_out(x, weight)
             y, rstd = ops.rmsnorm_fwd(x, weight.contiguous(), float(eps), half)
         else:  # (y, rstd) already computed from x (inverse_rms_norm)
             y, rstd = pre
@@ -136,9 +138,11 @@ def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module, pre=None):
     """``(x', norm(x))`` with x' = x for x's other use (see FusedRMSNormPass), on the
     fused kernels when ``norm`` is routed by ``enable_rmsnorm`` and x is a
     contiguous fp32 GPU tensor whose rows the vector kernels cover; otherwise
-    ``(x, norm(x))``.  ``pre``: the (y, rstd) ``inverse_rms_norm`` returned for x."""
+    ``(x, norm(x))`` (also for a norm weight that is not 16-byte aligned).  ``pre``:
+    the (y, rstd) ``inverse_rms_norm`` returned for x."""
     if (getattr(norm, "_rv_fused", False) and x.is_cuda and x.dtype == torch.float32
-            and x.is_contiguous() and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0):
+            and x.is_contiguous() and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0
+            and norm.weight.is_contiguous() and norm.weight.data_ptr() % 16 == 0):
         return FusedRMSNormPass.apply(x, norm.weight, rms_norm_eps(norm, x),
                                       getattr(norm, "_rv_fp16_out", False), pre)
     return x, norm(x)
@@ -151,7 +155,7 @@ def _sub_fusable(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module) -> boo
             and x.is_cuda and x.dtype == torch.float32
             and f.dtype in (torch.float16, torch.float32) and x.shape == f.shape
             and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
-            and _fp16_out(x))
+            and _fp16_out(x, norm.weight))
 
 
 def inverse_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
@@ -239,7 +243,7 @@ def add_rms_norm_pass(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module):
     if (getattr(norm, "_rv_fp16_out", False) and x.is_cuda and x.dtype == torch.float32
             and f.dtype == torch.float16 and x.shape == f.shape
             and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
-            and _fp16_out(x)):
+            and _fp16_out(x, norm.weight)):
         return FusedAddRMSNormPass.apply(x, f, norm.weight, rms_norm_eps(norm, x))
     return x.view_as(x), add_rms_norm(x, f, norm)[1]
 
@@ -253,7 +257,7 @@ def add_rms_norm(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module, pre=No
     if (getattr(norm, "_rv_fp16_out", False) and x.is_cuda and x.dtype == torch.float32
             and f.dtype in (torch.float16, torch.float32) and x.shape == f.shape
             and x.is_contiguous() and f.is_contiguous() and f.data_ptr() % 16 == 0
-            and _fp16_out(x)):
+            and _fp16_out(x, norm.weight)):
         return FusedAddRMSNorm.apply(x, f, norm.weight, rms_norm_eps(norm, x), pre)
     from .residual import euler_step
     h = euler_step(x, f, +1)

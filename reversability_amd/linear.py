@@ -14,7 +14,8 @@ reduces over all tokens in a fixed order, split-K when the output is small).
 
 ``enable_linear(model)`` patches every block's ``attn.qkv`` and ``attn.proj``;
 calls the kernels do not cover (no fp16 autocast, a bias, widths that are not
-multiples of 128, CPU tensors) keep ``F.linear``.
+multiples of 128, CPU tensors) keep ``F.linear``, recorded in ``paths.report()``
+(or raising under ``paths.strict()``).
 """
 from __future__ import annotations
 
@@ -24,6 +25,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
+from . import paths
 from ._hip import RV_F16, RV_F32, _check, _stream, library
 from .mlp import cast_f16, cast_weight
 
@@ -89,7 +91,14 @@ class FusedLinear(torch.autograd.Function):
 def linear(x: torch.Tensor, weight: torch.Tensor, bias=None) -> torch.Tensor:
     """``F.linear`` with the MFMA path where it applies."""
     if supported(x, weight, bias):
+        paths.took("linear", "mfma")
         return FusedLinear.apply(x, weight)
+    if x.is_cuda:
+        paths.took("linear", "torch",
+                   "MFMA projections need fp16 autocast, no bias and widths that are multiples "
+                   f"of 128 (weight {tuple(weight.shape)}, input {x.dtype})")
+    else:
+        paths.took("linear", "torch")
     return F.linear(x, weight, bias)
 
 

@@ -1,4 +1,4 @@
-"""Optimized midpoint training paths (src/reversibility/optimized.py:9-114).
+"""Optimized midpoint training paths (src/reversibility/optimized.py:9-101).
 
 ``ReusedMidpoint`` builds one force graph per layer in backward that serves both
 the inversion and the VJP: the current ``p`` IS the previous ``q``, so
@@ -15,7 +15,7 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
-from .residual import midpoint_step
+from .residual import eager_active, eager_updates, midpoint_step
 from .reversible import midpoint_terms
 
 
@@ -23,6 +23,7 @@ class ReusedMidpoint(torch.autograd.Function):
     @staticmethod
     def forward(ctx, p, q, blocks, h, *parameters):
         ctx.blocks, ctx.h = blocks, h
+        ctx.eager = eager_active()
         ctx.device = p.device.type
         ctx.amp = torch.is_autocast_enabled(ctx.device)
         ctx.dtype = torch.get_autocast_dtype(ctx.device)
@@ -39,7 +40,8 @@ class ReusedMidpoint(torch.autograd.Function):
         grads: list = []
         scale = 2 * ctx.h
         # No autocast weight-cast cache: see _InverseStack.backward.
-        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype, cache_enabled=False):
+        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype,
+                            cache_enabled=False), eager_updates(ctx.eager):
             for block in reversed(ctx.blocks):
                 with torch.enable_grad():
                     previous_q = p.detach().requires_grad_(True)
@@ -141,15 +143,3 @@ def _chunk_loss(logits, targets, loss_backend):
         return cross_entropy_sum(logits, targets)
     raise ValueError("Unknown loss backend")
 
-
-def cpu_snapshot(value):
-    """Independent CPU copies of a (nested) state (optimized.py:104-114)."""
-    if isinstance(value, torch.Tensor):
-        return value.detach().to("cpu", copy=True)
-    if isinstance(value, dict):
-        return {k: cpu_snapshot(v) for k, v in value.items()}
-    if isinstance(value, list):
-        return [cpu_snapshot(v) for v in value]
-    if isinstance(value, tuple):
-        return tuple(cpu_snapshot(v) for v in value)
-    return value

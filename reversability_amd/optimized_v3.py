@@ -25,9 +25,10 @@ import torch
 import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
+from . import paths as _paths
 from .kernels_v3 import add_rms_norm, add_rms_norm_pass, midpoint_rms_norm, rms_norm_pass
 from .optimized import ReusedMidpoint, amp_context, hidden_states
-from .residual import midpoint_step
+from .residual import eager_active, eager_updates, midpoint_step
 
 
 def mlp_value(x, up, down, fused):
@@ -88,6 +89,17 @@ def _use_mfma(x, up, down, fused, cdt):
     return fused and cdt == torch.float16 and mlp.supported(x, up, down)
 
 
+def _record_mlp_path(x, up, down, fused, cdt, mfma):
+    if mfma:
+        _paths.took("tiled_mlp", "mfma")
+    elif fused and x.is_cuda:
+        _paths.took("tiled_mlp", "torch-gemm",
+                    f"MFMA MLP needs fp16 compute and widths that are multiples of 128 "
+                    f"(d={x.shape[-1]}, f={down.shape[1]}, compute {cdt})")
+    else:  # the unfused computation the caller asked for, or a CPU tensor
+        _paths.took("tiled_mlp", "torch-gemm")
+
+
 class TiledMLP(torch.autograd.Function):
     """Save only the normalized input and weights; recompute token tiles in backward.
 
@@ -111,7 +123,14 @@ class TiledMLP(torch.autograd.Function):
         cdt = _compute_dtype(x, ctx.amp, ctx.dtype)
         flat = x.reshape(-1, x.shape[-1])
         output = torch.empty((flat.shape[0], down.shape[0]), device=x.device, dtype=cdt)
-        if _use_mfma(flat, up, down, fused, cdt):
+        mfma = _use_mfma(flat, up, down, fused, cdt)
+        _record_mlp_path(flat, up, down, fused, cdt, mfma)
+        if not need_output and not (keep_tiles and mfma):
+            # the output is only differentiated and there are no tiles to keep:
+            # nothing to compute (the backward recomputes its tiles)
+            ctx.save_for_backward(x, up, down)
+            return output.reshape(*x.shape[:-1], down.shape[0])
+        if mfma:
             from . import mlp
             # autocast's casts, once per call: the same fp16 values F.linear
             # would produce on every tile
@@ -189,17 +208,14 @@ class TiledMLP(torch.autograd.Function):
         return dx.reshape_as(x), dup, ddown, None, None, None, None
 
 
-# SplitMidpoint's backward evaluates each layer's attention twice on the same
-# input: under no_grad for the inversion, then again with gradients for its
-# VJP.  With this set the first evaluation is made with gradients and its graph
-# (one layer's attention, held through the MLP VJP) serves the VJP: the same
-# values, one attention evaluation per layer less.
-KEEP_SPLIT_ATTENTION = True
-
-
-# Each midpoint update made together with the attention norm of the layer that
-# reads it next (forward and reconstruction; same values).
-FUSE_MIDPOINT_NORM = True
+# The model's switches for SplitMidpoint (paths.ReconstructionPaths):
+#   keep_split_attention  the backward evaluates each layer's attention twice on
+#       the same input -- under no_grad for the inversion, then with gradients
+#       for its VJP; with the switch on, the first evaluation is made with
+#       gradients and its graph (one layer's attention, held through the MLP
+#       VJP) serves the VJP: the same values, one attention evaluation less;
+#   fuse_midpoint_norm    each midpoint update made together with the attention
+#       norm of the layer that reads it next (forward and reconstruction).
 
 
 class SplitMidpoint(torch.autograd.Function):
@@ -208,16 +224,19 @@ class SplitMidpoint(torch.autograd.Function):
     A detached attention proxy carries the force's dependence on attention, so
     the MLP graph can be released before the attention VJP.  The reference
     recomputes attention for that VJP (its disclosed extra-compute trade-off);
-    with KEEP_SPLIT_ATTENTION the inversion's attention graph is kept instead.
+    with the model's ``keep_split_attention`` the inversion's attention graph
+    is kept instead.
     """
 
     @staticmethod
     def forward(ctx, p, q, blocks, h, *parameters):
         ctx.blocks, ctx.h = blocks, h
+        ctx.eager = eager_active()
         ctx.device = p.device.type
         ctx.amp = torch.is_autocast_enabled(ctx.device)
         ctx.dtype = torch.get_autocast_dtype(ctx.device)
         from .reversible import midpoint_terms
+        fuse_norm = _paths.of(blocks).fuse_midpoint_norm
         normed = None  # the next block's attn_norm(q), made with the midpoint update
         for i, block in enumerate(blocks):
             if normed is None:
@@ -226,7 +245,7 @@ class SplitMidpoint(torch.autograd.Function):
                 attention = block.attn(normed)
                 mlp = block.mlp(add_rms_norm(q, attention, block.mlp_norm)[1])
             lower = blocks[i + 1] if i + 1 < len(blocks) else None
-            if FUSE_MIDPOINT_NORM and lower is not None:
+            if fuse_norm and lower is not None:
                 nxt, pre = midpoint_rms_norm(p, attention, mlp, 2 * h, +1, lower.attn_norm)
                 normed = pre[0] if pre is not None else None
             else:
@@ -242,15 +261,19 @@ class SplitMidpoint(torch.autograd.Function):
         p, q, *_ = ctx.saved_tensors
         grads: list = []
         scale = 2 * ctx.h
+        settings = _paths.of(ctx.blocks)
+        keep_attention = settings.keep_split_attention
+        fuse_norm = settings.fuse_midpoint_norm and keep_attention
         # No autocast weight-cast cache: the no_grad attention pass below would
         # otherwise leave history-free fp16 weight casts for the grad-enabled
         # rebuild (torch <= 2.10); casts are deterministic, values unchanged.
-        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype, cache_enabled=False):
+        with torch.autocast(ctx.device, enabled=ctx.amp, dtype=ctx.dtype,
+                            cache_enabled=False), eager_updates(ctx.eager):
             pre_p = None  # attn_norm(p) of this block, made with the previous inversion
             for index in reversed(range(len(ctx.blocks))):
                 block = ctx.blocks[index]
                 lower = ctx.blocks[index - 1] if index > 0 else None
-                if KEEP_SPLIT_ATTENTION:  # its graph serves the attention VJP below
+                if keep_attention:  # its graph serves the attention VJP below
                     with torch.enable_grad():
                         attn_input = p.detach().requires_grad_(True)
                         attn_pass, normed = rms_norm_pass(attn_input, block.attn_norm, pre_p)
@@ -265,7 +288,7 @@ class SplitMidpoint(torch.autograd.Function):
                     # gradients are summed in the norm's backward pass
                     q_pass, mlp_in = add_rms_norm_pass(previous_q, proxy, block.mlp_norm)
                     mlp = block.mlp(mlp_in)
-                    if FUSE_MIDPOINT_NORM and KEEP_SPLIT_ATTENTION and lower is not None:
+                    if fuse_norm and lower is not None:
                         # previous_p with the lower block's attn_norm of it
                         previous_p, pre_p = midpoint_rms_norm(q, proxy.detach(), mlp.detach(),
                                                               scale, -1, lower.attn_norm)
@@ -285,7 +308,7 @@ class SplitMidpoint(torch.autograd.Function):
                 mlp_grads = local[3:]
                 del proxy, mlp, next_q, local, q_pass, mlp_in
                 with torch.enable_grad():
-                    if not KEEP_SPLIT_ATTENTION:
+                    if not keep_attention:
                         attn_input = previous_q.detach().requires_grad_(True)
                         attn_pass, normed = rms_norm_pass(attn_input, block.attn_norm)
                         attention = block.attn(normed)
@@ -347,10 +370,13 @@ def _fused_head(hidden, weight, labels, denominator, chunk_tokens, scaler, preci
 
 
 def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsnorm=False,
-               keep_mlp_tiles=False):
+               keep_mlp_tiles=False, paths=None):
     """Wire the optimized core, tiled MLP, fused SwiGLU and fused RMSNorm
     (optimized_v3.py:120-148).  Idempotent for one configuration; raises on a
     conflicting reinstall, a non-midpoint optimized core, or a biased MLP.
+
+    ``paths`` (not in the reference): the model's reconstruction switches
+    (``paths.ReconstructionPaths``; default all on), recorded on the model.
 
     ``keep_mlp_tiles`` (not in the reference): a TiledMLP forward that runs with
     gradients enabled keeps its tiles' SwiGLU input and output for its backward
@@ -358,11 +384,13 @@ def install_v3(model, *, core_mode="reference", mlp_tokens=0, swiglu=False, rmsn
     one layer's tiles at a time (C5: 0.8 GB), and one up-projection GEMM per
     layer and step less; the kept values are the ones the recompute would
     produce, bit for bit."""
-    signature = (core_mode, mlp_tokens, swiglu, rmsnorm, keep_mlp_tiles)
+    settings = paths if paths is not None else _paths.DEFAULT
+    signature = (core_mode, mlp_tokens, swiglu, rmsnorm, keep_mlp_tiles, settings)
     if hasattr(model, "_v3_signature"):
         if model._v3_signature != signature:
             raise ValueError("Cannot replace an installed v3 configuration")
         return model
+    _paths.configure(model, settings)
     if core_mode != "reference":
         if getattr(model, "method", None) != "midpoint" or model.backward_mode != "reconstruct":
             raise ValueError("Optimized core requires reconstructed midpoint")
@@ -435,8 +463,15 @@ def _cached_head_backward(model, ids, labels, denominator, chunk_tokens, scaler,
     weight = model.lm_head.weight
     if (loss_backend in ("triton", "hip") and precision == "fp16" and ids.device.type == "cuda"
             and weight.dtype == torch.float32):
+        _paths.took("tied_head", "fused-ce+hipblaslt")
         return _fused_head(hidden, weight, labels, denominator, chunk_tokens, scaler, precision,
                            ids.device)
+    if loss_backend in ("triton", "hip") and ids.device.type == "cuda":
+        _paths.took("tied_head", "autograd-chunks",
+                    f"the fused head needs fp16 precision and an fp32 weight (got {precision}, "
+                    f"{weight.dtype})")
+    else:
+        _paths.took("tied_head", "autograd-chunks")
     leaf = hidden.detach().reshape(-1, hidden.shape[-1]).requires_grad_(True)
     if ids.device.type != "cuda" or precision == "fp32":
         dtype = weight.dtype

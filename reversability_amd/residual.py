@@ -11,8 +11,16 @@ ROCm tensors go through one HIP kernel per update (``rv_midpoint_update`` /
 ``rv_residual_axpy``); a missing library raises.  CPU tensors (the fp64 / fp32
 host-logic tests, and the reference's own CPU runs) evaluate the reference's
 eager expression, which is what the reference computes on CPU.
+
+``eager_updates()`` makes every update inside it (on this thread or task) the
+eager torch expression on any device: a model with its modules unpatched and
+``backward_mode='autograd'`` then runs as plain torch end to end -- the
+independent comparator the GPU parity tests hold the HIP path against.
 """
 from __future__ import annotations
+
+import contextlib
+import contextvars
 
 import torch
 from torch.autograd.function import once_differentiable
@@ -80,11 +88,32 @@ class EulerStep(torch.autograd.Function):
         return dout, df.to(ctx.force_dtype), None, None
 
 
+_EAGER = contextvars.ContextVar("reversability_amd_eager_updates", default=False)
+
+
+@contextlib.contextmanager
+def eager_updates(enabled: bool = True):
+    """Inside this block, ``midpoint_step`` / ``euler_step`` evaluate the
+    reference's eager torch expression on every device (no HIP kernel).
+    The reversible stack Functions record the mode of their forward and
+    re-enter it in their backward, which autograd runs on another thread."""
+    token = _EAGER.set(bool(enabled))
+    try:
+        yield
+    finally:
+        _EAGER.reset(token)
+
+
+def eager_active() -> bool:
+    """Whether ``eager_updates`` is in effect here."""
+    return _EAGER.get()
+
+
 def midpoint_step(p, a, m, scale, sign, graph_only=False):
     """p + sign * scale * (a + m) with the eager rounding points.  ``graph_only``
     (GPU only): the caller differentiates the result but never reads it, so the
     value is not computed (its memory is left as allocated)."""
-    if p.device.type == "cuda":
+    if p.device.type == "cuda" and not _EAGER.get():
         return MidpointStep.apply(p, a, m, scale, sign, graph_only)
     force = a + m
     return p + scale * force if sign > 0 else p - scale * force
@@ -92,6 +121,6 @@ def midpoint_step(p, a, m, scale, sign, graph_only=False):
 
 def euler_step(x, f, sign, graph_only=False):
     """x + sign * f (state dtype = x's); ``graph_only`` as midpoint_step's."""
-    if x.device.type == "cuda":
+    if x.device.type == "cuda" and not _EAGER.get():
         return EulerStep.apply(x, f, sign, graph_only)
     return x + f if sign > 0 else x - f

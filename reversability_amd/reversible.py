@@ -25,10 +25,11 @@ import math
 import torch
 from torch.autograd.function import once_differentiable
 
+from . import paths
 from .kernels_v3 import add_rms_norm, inverse_add_rms_norm, inverse_rms_norm, rms_norm_pass
 from .mlp import output_unused
 from .model import BaselineLM, Block, ModelConfig
-from .residual import euler_step, midpoint_step
+from .residual import eager_active, eager_updates, euler_step, midpoint_step
 
 
 def midpoint_terms(block: Block, x: torch.Tensor):
@@ -62,29 +63,28 @@ def inverse_pair(block, p, q, method, h):
     return previous_p, euler_step(q, block.attn(block.attn_norm(previous_p)), -1)
 
 
-# The Euler reconstruction evaluates A(p0) on the recovered p0 twice -- to
-# invert the step and again in the recompute for the VJP -- on identical bits.
-# With this set the inversion keeps that evaluation's graph for the VJP.
-REUSE_EULER_ATTENTION = True
-
-# The Euler inversion's subtractions p - M(q) and q - A(p0) computed in the
-# passes of the norms that read their results (same values).
-FUSE_EULER_INVERSE = True
-
-# The Euler VJP's rebuilt MLP output feeds only the graph-only next_p: with
-# this set, install_v3's tiled MLP does not compute it (same gradients).
-SKIP_UNUSED_MLP_OUTPUT = True
+# The model's switches of the reconstruction backward (paths.ReconstructionPaths):
+#   reuse_euler_attention   the Euler reconstruction evaluates A(p0) on the
+#       recovered p0 twice -- to invert the step and again in the recompute for
+#       the VJP -- on identical bits; the inversion keeps that evaluation's
+#       graph for the VJP (_euler_inverse_for_vjp);
+#   fuse_euler_inverse      the inversion's subtractions p - M(q) and q - A(p0)
+#       computed in the passes of the norms that read their results;
+#   skip_unused_mlp_output  the Euler VJP's rebuilt MLP output feeds only the
+#       graph-only next_p, so install_v3's tiled MLP does not compute it.
+# Each gives the same values as the plain inverse-then-recompute.
 
 
-def _euler_inverse_for_vjp(block, p, q):
+def _euler_inverse_for_vjp(block, p, q, settings):
     """Invert one Euler step and rebuild its graph with one evaluation of
     A(p0): p0 = p - M(q) (no graph), a = A(p0) with its graph, q0 = q - a, then
     next_q = q0 + a and next_p = p0 + M(next_q) as forward_pair computes them.
     Returns (next_p, next_q, p0, q0) with p0, q0 the graph's leaves; next_p is
     for differentiation only (on the GPU its value is not computed)."""
+    fuse = settings.fuse_euler_inverse
     with torch.no_grad():
         force = block.mlp(block.mlp_norm(q))
-        if FUSE_EULER_INVERSE:  # p0 and attn_norm(p0) in one pass
+        if fuse:  # p0 and attn_norm(p0) in one pass
             p0, pre_p0 = inverse_rms_norm(p, force, block.attn_norm)
         else:
             p0, pre_p0 = euler_step(p, force, -1), None
@@ -95,7 +95,7 @@ def _euler_inverse_for_vjp(block, p, q):
         # norm's backward pass (rms_norm_pass)
         p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0)
         attention = block.attn(normed_p0)
-        if FUSE_EULER_INVERSE:  # q0, q0 + A(p0) and its norm in one pass
+        if fuse:  # q0, q0 + A(p0) and its norm in one pass
             q0, pre_q = inverse_add_rms_norm(q, attention.detach(), block.mlp_norm)
         else:
             with torch.no_grad():
@@ -105,7 +105,7 @@ def _euler_inverse_for_vjp(block, p, q):
         next_q, normed = add_rms_norm(q0, attention, block.mlp_norm, pre_q)
         # next_p is only differentiated (its value is never read), and so is
         # the MLP output it adds: a tiled MLP skips its down projection
-        with output_unused() if SKIP_UNUSED_MLP_OUTPUT else contextlib.nullcontext():
+        with output_unused() if settings.skip_unused_mlp_output else contextlib.nullcontext():
             force = block.mlp(normed)
         next_p = euler_step(p0_pass, force, +1, graph_only=True)
     return next_p, next_q, p0, q0
@@ -117,6 +117,7 @@ class _InverseStack(torch.autograd.Function):
     @staticmethod
     def forward(ctx, p, q, blocks, method, h, *parameters):
         ctx.blocks, ctx.method, ctx.h = blocks, method, h
+        ctx.eager = eager_active()
         ctx.device_type = p.device.type
         ctx.amp_enabled = torch.is_autocast_enabled(ctx.device_type)
         ctx.amp_dtype = torch.get_autocast_dtype(ctx.device_type)
@@ -130,15 +131,16 @@ class _InverseStack(torch.autograd.Function):
     def backward(ctx, dp, dq):
         p, q, *_ = ctx.saved_tensors
         grads: list = []
+        settings = paths.of(ctx.blocks)
         # cache_enabled=False: torch <= 2.10 caches autocast weight casts made
         # under no_grad (the inverse below) and hands them, without autograd
         # history, to the grad-enabled recompute.  Casts are deterministic, so
         # skipping the cache changes no value.
         with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype,
-                            cache_enabled=False):
+                            cache_enabled=False), eager_updates(ctx.eager):
             for block in reversed(ctx.blocks):
-                if ctx.method == "euler" and REUSE_EULER_ATTENTION:
-                    next_p, next_q, p0, q0 = _euler_inverse_for_vjp(block, p, q)
+                if ctx.method == "euler" and settings.reuse_euler_attention:
+                    next_p, next_q, p0, q0 = _euler_inverse_for_vjp(block, p, q, settings)
                 else:
                     with torch.no_grad():
                         p0, q0 = inverse_pair(block, p, q, ctx.method, ctx.h)

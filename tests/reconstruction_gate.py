@@ -1,31 +1,40 @@
-"""Reconstruction / gradient gate, restated from scripts/validate_reversible.py:18-118.
+"""Reconstruction / gradient gate for the reversible core, written from the
+procedure of the reference's gate (scripts/validate_reversible.py:18-118).
 
-``check_case`` compares, for one (method, precision, device, depth, length):
+A case builds one seeded ``ReversibleLM`` -- the *candidate*: reconstruction
+backward, optionally with this repository's fused paths installed by a
+``prepare`` hook -- and a deep copy made before ``prepare`` runs -- the
+*comparator*: modules unpatched, ``backward_mode='autograd'``, and every
+residual update evaluated as the eager torch expression
+(``residual.eager_updates``), so it is plain torch end to end.
 
-1. every state reconstructed by ``inverse_pair`` against the state recorded by
-   the no-grad forward (validate_reversible.py:55-63);
-2. ``ReversibleLM.core`` (reconstruction backward) against an independent
-   eager restatement of the recurrence differentiated by ordinary autograd:
-   outputs, input gradient and every parameter gradient (:64-83);
-3. logits and loss of the two models (:85-90);
-4. full-model gradients and one clipped AdamW step, coordinatewise and as a
-   relative L2 of the update (:91-116).
+Four stages compare the two, each quantity against the tolerance tables of the
+reference's policy (kept as they are: they are the parity bar):
 
-The tolerance tables are the reference's (validate_reversible.py:20-29).
-``models`` lets a caller pass a candidate built some other way (e.g. with the
-fused HIP kernels installed) next to the plain autograd reference.
+  states   a no-grad forward records every (p, q); ``inverse_pair`` walks back
+           from the last pair and each rebuilt pair must match the record;
+  core     the candidate stack's output, input gradient and parameter gradients
+           under a random probe, against an equation-level restatement of the
+           recurrence (``eager_core``) differentiated by autograd;
+  model    logits and mean cross-entropy with one ignored target;
+  update   full-model gradients (GradScaler-scaled under fp16), clip at 1.0 and
+           one AdamW step: every parameter coordinatewise (optimizer table) and
+           the whole update's relative L2.
 """
 from __future__ import annotations
 
 import contextlib
 import copy
+import dataclasses
 
 import torch
 import torch.nn.functional as F
 
 from reversability_amd import ModelConfig, ReversibleLM
+from reversability_amd.residual import eager_updates
 from reversability_amd.reversible import forward_pair, inverse_pair
 
+# scripts/validate_reversible.py:20-29 (policy "reconstruction-gradient-v2")
 OPTIMIZER_TOLERANCES = {"fp64": {"atol": 1e-9, "rtol": 1e-8},
                         "fp32": {"atol": 5e-5, "rtol": 3e-4},
                         "fp16": {"atol": 1.2e-3, "rtol": 0.0}}
@@ -34,117 +43,167 @@ TOLERANCES = {"fp64": {"atol": 1e-9, "rtol": 1e-8},
               "fp32": {"atol": 3e-5, "rtol": 3e-4},
               "fp16": {"atol": 5e-3, "rtol": 5e-2}}
 
+# The reference's CUDA case list (scripts/validate_reversible.py:134-141):
+# three (depth, length) shapes, midpoint at two step sizes, two seeds, plus the
+# architecture-sized probe (7 layers x 512 tokens x width 256, 8 heads).
+GRID_SHAPES = ((1, 8), (3, 17), (7, 32))
+GRID_SEEDS = (1337, 2026)
+MIDPOINT_STEPS = (0.25, 0.5)
 
-def reference_core(model, x, method, h):
-    """The recurrence written out with eager torch ops (validate_reversible.py:65-73)."""
-    p, q = x, x
-    for b in model.blocks:
-        if method == "midpoint":
-            a = b.attn(b.attn_norm(q))
-            force = a + b.mlp(b.mlp_norm(q + a))
-            p, q = q, p + (2 * h) * force
+
+def step_sizes(method):
+    return MIDPOINT_STEPS if method == "midpoint" else (0.5,)
+
+
+def eager_core(model, x, method, h):
+    """The integrator written as equations over the model's submodules."""
+    p = q = x
+    for block in model.blocks:
+        if method == "euler":
+            q = q + block.attn(block.attn_norm(p))
+            p = p + block.mlp(block.mlp_norm(q))
+            continue
+        attention = block.attn(block.attn_norm(q))
+        force = attention + block.mlp(block.mlp_norm(q + attention))
+        p, q = q, p + (2 * h) * force
+    return p if method == "euler" else q
+
+
+@dataclasses.dataclass
+class GateReport:
+    method: str
+    precision: str
+    depth: int
+    length: int
+    width: int
+    step_size: float
+    seed: int
+    errors: dict = dataclasses.field(default_factory=dict)
+
+    def check(self, name, actual, expected):
+        """Record max-abs and relative error of ``actual`` and assert the policy."""
+        actual, expected = actual.detach(), expected.detach()
+        assert torch.isfinite(actual).all(), f"{name}: non-finite candidate"
+        assert torch.isfinite(expected).all(), f"{name}: non-finite comparator"
+        worst = (actual - expected).abs().max().item() if actual.numel() else 0.0
+        scale = expected.abs().max().item() if expected.numel() else 0.0
+        self.errors[name] = {"max_abs": worst,
+                             "relative_to_max_reference": worst / max(scale, 1e-12)}
+        table = OPTIMIZER_TOLERANCES if name.startswith("optimizer_") else TOLERANCES
+        torch.testing.assert_close(actual, expected, **table[self.precision], msg=name)
+
+    def worst_state_error(self) -> float:
+        return max(v["max_abs"] for k, v in self.errors.items() if k.startswith("state_"))
+
+
+def _autocast(precision):
+    if precision == "fp16":
+        return torch.autocast(device_type="cuda", dtype=torch.float16)
+    return contextlib.nullcontext()
+
+
+def _stage_states(report, model, x, method, h, precision):
+    with _autocast(precision), torch.no_grad():
+        record = [(x, x)]
+        for block in model.blocks:
+            record.append(forward_pair(block, *record[-1], method, h))
+        pair = record[-1]
+        for index in reversed(range(len(model.blocks))):
+            pair = inverse_pair(model.blocks[index], *pair, method, h)
+            report.check(f"state_{index}_p", pair[0], record[index][0])
+            report.check(f"state_{index}_q", pair[1], record[index][1])
+
+
+def _stage_core(report, candidate, comparator, x, method, h, precision):
+    leaves = [x.detach().clone().requires_grad_(True) for _ in range(2)]
+    with _autocast(precision):
+        out = candidate.core(leaves[0])
+        with eager_updates():
+            expected = eager_core(comparator, leaves[1], method, h)
+        report.check("core_output", out, expected)
+        probe = torch.randn_like(out)
+        for value, leaf in ((out, leaves[0]), (expected, leaves[1])):
+            (value * probe).mean().backward()
+    report.check("input_gradient", leaves[0].grad, leaves[1].grad)
+    theirs = dict(comparator.named_parameters())
+    for name, param in candidate.named_parameters():
+        if param.grad is not None:
+            report.check("core_gradient_" + name, param.grad, theirs[name].grad)
+
+
+def _stage_model(report, candidate, comparator, ids, labels, precision):
+    losses = []
+    with _autocast(precision):
+        for model, eager in ((candidate, False), (comparator, True)):
+            with eager_updates() if eager else contextlib.nullcontext():
+                logits = model(ids)
+            losses.append((logits, F.cross_entropy(logits.flatten(0, 1), labels.flatten())))
+        report.check("logits", losses[0][0], losses[1][0])
+        report.check("loss", losses[0][1], losses[1][1])
+    return [loss for _, loss in losses]
+
+
+def _stage_update(report, candidate, comparator, losses, precision):
+    pair = (candidate, comparator)
+    optimizers = [torch.optim.AdamW(m.parameters(), lr=6e-4, betas=(.9, .95), weight_decay=.1)
+                  for m in pair]
+    scalers = ([torch.amp.GradScaler("cuda") for _ in pair] if precision == "fp16"
+               else [None, None])
+    for loss, opt, scaler in zip(losses, optimizers, scalers):
+        if scaler is None:
+            loss.backward()
         else:
-            q = q + b.attn(b.attn_norm(p))
-            p = p + b.mlp(b.mlp_norm(q))
-    return q if method == "midpoint" else p
+            scaler.scale(loss).backward()
+            scaler.unscale_(opt)
+    named = list(zip(candidate.named_parameters(), comparator.named_parameters()))
+    for (name, mine), (other_name, theirs) in named:
+        assert name == other_name and mine.grad is not None and theirs.grad is not None, name
+        report.check("gradient_" + name, mine.grad, theirs.grad)
+    start = [p.detach().clone() for p in comparator.parameters()]
+    for model, opt, scaler in zip(pair, optimizers, scalers):
+        assert torch.isfinite(torch.nn.utils.clip_grad_norm_(model.parameters(), 1.0))
+        if scaler is None:
+            opt.step()
+            continue
+        scale = scaler.get_scale()
+        scaler.step(opt)
+        scaler.update()
+        assert scaler.get_scale() >= scale, "loss-scale overflow in the update stage"
+    for (name, mine), (_, theirs) in named:
+        report.check("optimizer_" + name, mine, theirs)
+    gap = sum(float((a.detach() - b.detach()).double().square().sum())
+              for a, b in zip(candidate.parameters(), comparator.parameters()))
+    moved = sum(float((b.detach() - b0).double().square().sum())
+                for b, b0 in zip(comparator.parameters(), start))
+    relative = (gap / max(moved, 1e-30)) ** .5
+    report.errors["optimizer_relative_update_l2"] = relative
+    assert relative <= UPDATE_RELATIVE_L2[report.precision], ("update relative L2", relative)
 
 
-def check_case(method, precision, device, depth, length, width=32, heads=2, h=0.5, seed=1337,
-               prepare=None):
-    """Run the gate; ``prepare(model)`` may install optimized paths on the
-    candidate.  Returns the error report; raises AssertionError on failure."""
+def run_gate(method, precision, device, depth, length, width=32, heads=2, h=0.5, seed=1337,
+             prepare=None) -> GateReport:
+    """One gate case; raises AssertionError on the first quantity outside the
+    policy.  ``prepare(candidate)`` installs optional paths on the candidate."""
     torch.manual_seed(seed)
     config = ModelConfig(vocab_size=101, max_sequence_length=length, n_layers=depth,
                          n_heads=heads, d_model=width, d_ff=4 * width)
     dtype = torch.float64 if precision == "fp64" else torch.float32
     candidate = ReversibleLM(config, method, h).to(device=device, dtype=dtype)
-    reference = copy.deepcopy(candidate)
-    reference.backward_mode = "autograd"
+    comparator = copy.deepcopy(candidate)
+    comparator.backward_mode = "autograd"
     if prepare is not None:
         prepare(candidate)
-    amp = ((lambda: torch.autocast(device_type="cuda", dtype=torch.float16))
-           if precision == "fp16" else contextlib.nullcontext)
-    errors = {}
-
-    def compare(name, actual, expected):
-        assert torch.isfinite(actual).all() and torch.isfinite(expected).all(), name
-        delta = (actual.detach() - expected.detach()).abs()
-        errors[name] = {"max_abs": delta.max().item(),
-                        "relative_to_max_reference":
-                            delta.max().item() / max(expected.detach().abs().max().item(), 1e-12)}
-        policy = OPTIMIZER_TOLERANCES if name.startswith("optimizer_") else TOLERANCES
-        torch.testing.assert_close(actual, expected, **policy[precision], msg=name)
-
     ids = torch.randint(0, config.vocab_size, (2, length), device=device)
     labels = torch.randint(0, config.vocab_size, (2, length), device=device)
-    labels[-1, -1] = -100
-    with amp(), torch.no_grad():
-        x = candidate.token_embedding(ids) + candidate.position_embedding(
+    labels[-1, -1] = -100  # a partial-target normalization
+    report = GateReport(method, precision, depth, length, width, h, seed)
+    with torch.no_grad():
+        x = comparator.token_embedding(ids) + comparator.position_embedding(
             torch.arange(length, device=device))
-        p, q = x, x
-        states = [(p, q)]
-        for block in candidate.blocks:
-            p, q = forward_pair(block, p, q, method, h)
-            states.append((p, q))
-        for i in range(depth - 1, -1, -1):
-            p, q = inverse_pair(candidate.blocks[i], p, q, method, h)
-            compare(f"state_{i}_p", p, states[i][0])
-            compare(f"state_{i}_q", q, states[i][1])
-    with amp():
-        x1 = x.detach().requires_grad_(True)
-        x2 = x.detach().requires_grad_(True)
-        out1 = candidate.core(x1)
-        out2 = reference_core(reference, x2, method, h)
-        compare("core_output", out1, out2)
-        probe = torch.randn_like(out1)
-        (out1 * probe).mean().backward()
-        (out2 * probe).mean().backward()
-        compare("input_gradient", x1.grad, x2.grad)
-    ref_params = dict(reference.named_parameters())
-    for name, p1 in candidate.named_parameters():
-        if p1.grad is not None:
-            compare("core_gradient_" + name, p1.grad, ref_params[name].grad)
+    _stage_states(report, candidate, x, method, h, precision)
+    _stage_core(report, candidate, comparator, x, method, h, precision)
     candidate.zero_grad()
-    reference.zero_grad()
-    with amp():
-        logits1 = candidate(ids)
-        logits2 = reference(ids)
-        compare("logits", logits1, logits2)
-        loss1 = F.cross_entropy(logits1.flatten(0, 1), labels.flatten())
-        loss2 = F.cross_entropy(logits2.flatten(0, 1), labels.flatten())
-        compare("loss", loss1, loss2)
-    optimizers = [torch.optim.AdamW(m.parameters(), lr=6e-4, betas=(.9, .95), weight_decay=.1)
-                  for m in (candidate, reference)]
-    scalers = [torch.amp.GradScaler("cuda") for _ in optimizers] if precision == "fp16" else None
-    if scalers:
-        for scaler, opt, loss in zip(scalers, optimizers, (loss1, loss2)):
-            scaler.scale(loss).backward()
-            scaler.unscale_(opt)
-    else:
-        loss1.backward()
-        loss2.backward()
-    for (name, p1), (name2, p2) in zip(candidate.named_parameters(), reference.named_parameters()):
-        assert name == name2 and p1.grad is not None and p2.grad is not None
-        compare("gradient_" + name, p1.grad, p2.grad)
-    before = {name: p.detach().clone() for name, p in reference.named_parameters()}
-    for i, (m, opt) in enumerate(zip((candidate, reference), optimizers)):
-        norm = torch.nn.utils.clip_grad_norm_(m.parameters(), 1.0)
-        assert torch.isfinite(norm)
-        if scalers:
-            old = scalers[i].get_scale()
-            scalers[i].step(opt)
-            scalers[i].update()
-            assert scalers[i].get_scale() >= old, "overflow in optimizer gate"
-        else:
-            opt.step()
-    for (name, p1), (_, p2) in zip(candidate.named_parameters(), reference.named_parameters()):
-        compare("optimizer_" + name, p1, p2)
-    diff_sq = sum((a.detach() - b.detach()).double().square().sum().item()
-                  for a, b in zip(candidate.parameters(), reference.parameters()))
-    update_sq = sum((p.detach() - before[name]).double().square().sum().item()
-                    for name, p in reference.named_parameters())
-    relative = (diff_sq / max(update_sq, 1e-30)) ** .5
-    errors["optimizer_relative_update_l2"] = relative
-    assert relative <= UPDATE_RELATIVE_L2[precision], ("optimizer update L2", relative)
-    return {"method": method, "precision": precision, "depth": depth, "length": length,
-            "width": width, "errors": errors}
+    comparator.zero_grad()
+    losses = _stage_model(report, candidate, comparator, ids, labels, precision)
+    _stage_update(report, candidate, comparator, losses, precision)
+    return report

@@ -502,3 +502,38 @@ def test_fused_add_rmsnorm_pass_matches_composition(cuda_device, rows, width):
             assert torch.allclose(a, b, rtol=1e-5, atol=1e-6)
         else:
             assert torch.equal(a, b), i
+
+
+@pytest.mark.parametrize("width", [256, 1024])
+def test_fused_norm_paths_with_unaligned_weight_take_the_unfused_path(cuda_device, width):
+    """A norm weight that sits 4 bytes past a 16-byte boundary (a view into a
+    shared buffer): the fused fp16-output norm paths (inverse_rms_norm,
+    inverse_add_rms_norm, midpoint_rms_norm, add_rms_norm, rms_norm_pass) fall
+    back to the unfused composition instead of raising, and give its values."""
+    from reversability_amd.kernels_v3 import (add_rms_norm, enable_rmsnorm, inverse_add_rms_norm,
+                                              inverse_rms_norm, midpoint_rms_norm, rms_norm_pass)
+    g = torch.Generator().manual_seed(31)
+    buf = torch.randn(width + 4, generator=g).to(cuda_device)
+    norm = torch.nn.RMSNorm(width).to(cuda_device)
+    norm.weight = torch.nn.Parameter(buf[1:width + 1])
+    assert norm.weight.data_ptr() % 16 != 0
+    enable_rmsnorm(norm, fp16_out=True)
+    x = torch.randn(64, width, generator=g).to(cuda_device)
+    f = torch.randn(64, width, generator=g).to(cuda_device).half()
+    m = torch.randn(64, width, generator=g).to(cuda_device).half()
+    with torch.autocast("cuda", dtype=torch.float16):
+        d, pre = inverse_rms_norm(x, f, norm)
+        assert pre is None and torch.equal(d, x - f)
+        d, pre = inverse_add_rms_norm(x, f, norm)
+        assert pre is None and torch.equal(d, x - f)
+        out, pre = midpoint_rms_norm(x, f, m, 1.0, 1, norm)
+        assert pre is None
+        assert torch.equal(out, x + (f + m) * 1.0)
+        h, y = add_rms_norm(x, f, norm)
+        assert torch.equal(h, x + f)
+        ref = F.rms_norm(h, (width,), norm.weight.detach(), eps=torch.finfo(torch.float32).eps)
+        assert (y.float() - ref).abs().max() <= 1e-5 * ref.abs().max() + 1e-3
+        leaf = x.clone().requires_grad_(True)
+        passed, y2 = rms_norm_pass(leaf, norm)
+        (passed.sum() + y2.float().sum()).backward()
+    assert torch.isfinite(leaf.grad).all()

@@ -13,6 +13,7 @@ Bars (north star / the reference's own gates)
 """
 from __future__ import annotations
 
+import contextlib
 import copy
 import math
 
@@ -21,13 +22,15 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from reconstruction_gate import TOLERANCES, check_case
-from reversability_amd import build_model
+from reconstruction_gate import (GRID_SEEDS, GRID_SHAPES, TOLERANCES, run_gate,
+                                  step_sizes)
+from reversability_amd import build_model, paths
 from reversability_amd.attention import enable_attention
 from reversability_amd.embedding import enable_embedding
 from reversability_amd.kernels_v3 import FusedRMSNorm
 from reversability_amd.linear import enable_linear
 from reversability_amd.optimized_v3 import TiledMLP, cached_head_backward, install_v3
+from reversability_amd.residual import eager_updates
 from reversability_amd.reversible import forward_pair, inverse_pair
 
 pytestmark = pytest.mark.gpu
@@ -46,8 +49,14 @@ def rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
 @pytest.mark.parametrize("method", ["midpoint", "euler"])
 @pytest.mark.parametrize("precision", ["fp64", "fp32", "fp16"])
 def test_reconstruction_gate_plain(cuda_device, method, precision):
-    for depth, length in [(1, 8), (3, 17), (7, 32)]:
-        check_case(method, precision, cuda_device, depth, length)
+    """The reference's CUDA grid (validate_reversible.py:134-139): three shapes,
+    midpoint at h = 0.25 and 0.5, seeds 1337 and 2026 -- 54 cases over the
+    parametrization; the candidate runs its residual updates on the HIP
+    kernels, the comparator is plain torch."""
+    for depth, length in GRID_SHAPES:
+        for h in step_sizes(method):
+            for seed in GRID_SEEDS:
+                run_gate(method, precision, cuda_device, depth, length, h=h, seed=seed)
 
 
 def _install_all(method):
@@ -62,26 +71,72 @@ def _install_all(method):
 @pytest.mark.parametrize("method", ["midpoint", "euler"])
 @pytest.mark.parametrize("precision", ["fp32", "fp16"])
 def test_reconstruction_gate_fused_v3(cuda_device, method, precision):
-    check_case(method, precision, cuda_device, 3, 17, prepare=_install_all(method))
+    for h in step_sizes(method):
+        run_gate(method, precision, cuda_device, 3, 17, h=h, prepare=_install_all(method))
 
 
 @pytest.mark.parametrize("core", ["reuse", "split"])
 def test_reconstruction_gate_optimized_cores_fp16(cuda_device, core):
-    check_case("midpoint", "fp16", cuda_device, 3, 17,
-               prepare=lambda m: install_v3(m, core_mode=core, swiglu=True, rmsnorm=True))
+    run_gate("midpoint", "fp16", cuda_device, 3, 17,
+             prepare=lambda m: install_v3(m, core_mode=core, swiglu=True, rmsnorm=True))
+
+
+# Worst reconstructed-state errors the reference recorded on its GPU (T4) for the
+# 7 x 512 x 256 probe (results/recorded/reversible-v1/correctness/cuda.json):
+# fp16 AMP 7.63e-5 (midpoint) / 9.54e-5 (Euler), fp32 1.30e-7 / 1.36e-7.  The
+# seeded inputs differ between CUDA and ROCm generators, so the measured value
+# here is held to 4x the recorded one (a tracking bar well inside the gate's
+# atol) rather than to equality.
+RECORDED_PROBE_STATE_ERROR = {("midpoint", "fp16"): 7.63e-5, ("euler", "fp16"): 9.54e-5,
+                              ("midpoint", "fp32"): 1.30e-7, ("euler", "fp32"): 1.36e-7}
 
 
 @pytest.mark.parametrize("method", ["midpoint", "euler"])
-@pytest.mark.parametrize("precision", ["fp32", "fp16"])
-def test_architecture_sized_probe(cuda_device, method, precision):
-    """validate_reversible.py:141: 7 layers x 512 tokens x width 256, 8 heads."""
-    report = check_case(method, precision, cuda_device, 7, 512, width=256, heads=8,
-                        prepare=_install_all(method))
-    worst = max(v["max_abs"] for k, v in report["errors"].items() if k.startswith("state_"))
-    # The reference recorded (T4, fp16 AMP) worst state errors of 7.63e-5
-    # (midpoint) and 9.54e-5 (Euler); the gate itself is atol 5e-3.
-    print(f"\n[probe] {method} {precision} worst reconstructed-state max-abs {worst:.3e}", flush=True)
+@pytest.mark.parametrize("precision", ["fp64", "fp32", "fp16"])
+@pytest.mark.parametrize("wiring", ["plain", "v3"])
+def test_architecture_sized_probe(cuda_device, method, precision, wiring):
+    """validate_reversible.py:141: 7 layers x 512 tokens x width 256, 8 heads --
+    the plain model (HIP residual updates) and the v3 wiring (fused norms,
+    SwiGLU, tiled MFMA MLP; fp32/fp16 only: the fused operators are fp32/fp16)."""
+    if wiring == "v3" and precision == "fp64":
+        pytest.skip("the fused v3 operators take fp32 / fp16 tensors")
+    report = run_gate(method, precision, cuda_device, 7, 512, width=256, heads=8,
+                      prepare=_install_all(method) if wiring == "v3" else None)
+    worst = report.worst_state_error()
+    print(f"\n[probe] {method} {precision} {wiring} worst reconstructed-state max-abs "
+          f"{worst:.3e}", flush=True)
     assert worst < TOLERANCES[precision]["atol"]
+    recorded = RECORDED_PROBE_STATE_ERROR.get((method, precision))
+    if recorded is not None:
+        assert worst < 4 * recorded, (worst, recorded)
+
+
+@pytest.mark.parametrize("method", ["midpoint", "euler"])
+def test_comparator_is_plain_torch(cuda_device, monkeypatch, method):
+    """Under residual.eager_updates an unpatched model in autograd mode (the
+    comparator of the gates below) reaches none of the HIP residual kernels:
+    with their autograd Functions made to raise, its fp16 forward + backward
+    still runs, and its loss equals the same model's under autograd with the
+    HIP residual kernels to fp16-autocast tolerance."""
+    from reversability_amd import residual
+    torch.manual_seed(5)
+    cfg = {"model": {"vocab_size": 101, "max_sequence_length": 64, "n_layers": 3,
+                     "n_heads": 4, "d_model": 128, "d_ff": 256}, "method": method}
+    model = build_model(cfg).to(cuda_device)
+    model.backward_mode = "autograd"
+    ids = torch.randint(0, 101, (2, 64), device=cuda_device)
+    with torch.autocast("cuda", dtype=torch.float16):
+        with_kernels = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+
+    def refuse(*args, **kwargs):
+        raise AssertionError("the comparator reached a HIP residual kernel")
+    monkeypatch.setattr(residual.MidpointStep, "apply", refuse)
+    monkeypatch.setattr(residual.EulerStep, "apply", refuse)
+    with torch.autocast("cuda", dtype=torch.float16), eager_updates():
+        loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+    loss.backward()
+    assert all(p.grad is not None for p in model.parameters())
+    assert abs(loss.item() - with_kernels.item()) <= 2e-3 * abs(loss.item())
 
 
 # --------------------------------------------------------------------------
@@ -209,11 +264,15 @@ def _c4_batch(device, batch=33, length=512):
     return x, y
 
 
-def _step_grads(model, x, y):
+def _step_grads(model, x, y, eager=False):
+    """Loss and unscaled gradients of one fp16-autocast step; ``eager``: the
+    model's residual updates as the eager torch expression (the comparator)."""
     scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 10)
     model.zero_grad(set_to_none=True)
     with torch.autocast("cuda", dtype=torch.float16):
-        loss = F.cross_entropy(model(x).flatten(0, 1), y.flatten(), reduction="sum") / y.numel()
+        with eager_updates() if eager else contextlib.nullcontext():
+            logits = model(x)
+        loss = F.cross_entropy(logits.flatten(0, 1), y.flatten(), reduction="sum") / y.numel()
     scaler.scale(loss).backward()
     inv = 1.0 / scaler.get_scale()
     return loss.detach(), {n: p.grad.detach() * inv for n, p in model.named_parameters()}
@@ -227,7 +286,7 @@ def test_full_midpoint_step_matches_autograd(cuda_device, core):
     reference.backward_mode = "autograd"
     install_v3(candidate, core_mode=core, mlp_tokens=8192, swiglu=True, rmsnorm=True)
     x, y = _c4_batch(cuda_device)
-    loss_r, grads_r = _step_grads(reference, x, y)
+    loss_r, grads_r = _step_grads(reference, x, y, eager=True)
     loss_c, grads_c = _step_grads(candidate, x, y)
     print(f"\n[c4] core={core} loss candidate {loss_c.item():.6f} eager {loss_r.item():.6f}",
           flush=True)
@@ -270,7 +329,7 @@ def test_bench_path_step_matches_autograd(cuda_device):
     enable_attention(candidate)
     enable_embedding(candidate, into_grad=True)
     x, y = _c4_batch(cuda_device)
-    loss_r, grads_r = _step_grads(reference, x, y)
+    loss_r, grads_r = _step_grads(reference, x, y, eager=True)
     scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 10)
     candidate.zero_grad(set_to_none=True)
     total = cached_head_backward(candidate, x, y, y.numel(), y.numel(), scaler, "fp16", False,
@@ -346,7 +405,6 @@ def test_euler_attention_reuse_bitwise(cuda_device):
     """The Euler reconstruction with the inversion's A(p0) reused for the VJP
     gives the same loss and gradients, bit for bit, as inverting and then
     recomputing the step."""
-    from reversability_amd import reversible
     torch.manual_seed(11)
     cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
                      "d_model": 256, "d_ff": 512}, "method": "euler", "step_size": 0.5}
@@ -357,30 +415,25 @@ def test_euler_attention_reuse_bitwise(cuda_device):
     enable_attention(model)
     ids = torch.randint(0, 512, (2, 256), device=cuda_device)
     runs = []
-    saved = reversible.REUSE_EULER_ATTENTION
-    try:
-        for reuse in (False, True):
-            reversible.REUSE_EULER_ATTENTION = reuse
-            model.zero_grad(set_to_none=True)
-            with torch.autocast("cuda", dtype=torch.float16):
-                loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
-            loss.backward()
-            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
-    finally:
-        reversible.REUSE_EULER_ATTENTION = saved
+    for reuse in (False, True):
+        paths.configure(model, reuse_euler_attention=reuse)
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+        loss.backward()
+        runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("switch", ["SKIP_UNUSED_MLP_OUTPUT", "FUSE_EULER_INVERSE"])
+@pytest.mark.parametrize("switch", ["skip_unused_mlp_output", "fuse_euler_inverse"])
 @pytest.mark.parametrize("keep_tiles", [False, True])
 def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch):
     """The Euler VJP's rebuilt MLP output only feeds the graph-only next_p
-    (SKIP_UNUSED_MLP_OUTPUT), and the inversion's subtractions can run inside
-    the norms that read them (FUSE_EULER_INVERSE): either switch leaves the
+    (skip_unused_mlp_output), and the inversion's subtractions can run inside
+    the norms that read them (fuse_euler_inverse): either switch leaves the
     loss and every gradient unchanged, bit for bit."""
-    from reversability_amd import reversible
     torch.manual_seed(13)
     cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
                      "d_model": 256, "d_ff": 512}, "method": "euler", "step_size": 0.5}
@@ -391,17 +444,13 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch
     enable_attention(model)
     ids = torch.randint(0, 512, (2, 256), device=cuda_device)
     runs = []
-    saved = getattr(reversible, switch)
-    try:
-        for on in (False, True):
-            setattr(reversible, switch, on)
-            model.zero_grad(set_to_none=True)
-            with torch.autocast("cuda", dtype=torch.float16):
-                loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
-            loss.backward()
-            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
-    finally:
-        setattr(reversible, switch, saved)
+    for on in (False, True):
+        paths.configure(model, **{switch: on})
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+        loss.backward()
+        runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)
@@ -409,9 +458,8 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch
 
 def test_split_midpoint_fused_update_norm_bitwise(cuda_device):
     """The split midpoint core with each midpoint update made together with
-    the next layer's attention norm (FUSE_MIDPOINT_NORM) gives the same loss
+    the next layer's attention norm (fuse_midpoint_norm) gives the same loss
     and gradients, bit for bit, as the separate update and norm."""
-    from reversability_amd import optimized_v3
     torch.manual_seed(17)
     cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 4,
                      "d_model": 256, "d_ff": 512}, "method": "midpoint", "step_size": 0.5}
@@ -422,17 +470,13 @@ def test_split_midpoint_fused_update_norm_bitwise(cuda_device):
     enable_attention(model)
     ids = torch.randint(0, 512, (2, 256), device=cuda_device)
     runs = []
-    saved = optimized_v3.FUSE_MIDPOINT_NORM
-    try:
-        for on in (False, True):
-            optimized_v3.FUSE_MIDPOINT_NORM = on
-            model.zero_grad(set_to_none=True)
-            with torch.autocast("cuda", dtype=torch.float16):
-                loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
-            loss.backward()
-            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
-    finally:
-        optimized_v3.FUSE_MIDPOINT_NORM = saved
+    for on in (False, True):
+        paths.configure(model, fuse_midpoint_norm=on)
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+        loss.backward()
+        runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)
@@ -441,7 +485,6 @@ def test_split_midpoint_fused_update_norm_bitwise(cuda_device):
 def test_split_midpoint_kept_attention_bitwise(cuda_device):
     """SplitMidpoint with the inversion's attention graph kept for the attention
     VJP gives the same loss and gradients, bit for bit, as recomputing it."""
-    from reversability_amd import optimized_v3
     torch.manual_seed(12)
     model = build_model(C4).to(cuda_device)
     install_v3(model, core_mode="split", mlp_tokens=8192, swiglu=True, rmsnorm=True,
@@ -450,17 +493,13 @@ def test_split_midpoint_kept_attention_bitwise(cuda_device):
     enable_attention(model)
     x, y = _c4_batch(cuda_device, batch=4)
     runs = []
-    saved = optimized_v3.KEEP_SPLIT_ATTENTION
-    try:
-        for keep in (False, True):
-            optimized_v3.KEEP_SPLIT_ATTENTION = keep
-            model.zero_grad(set_to_none=True)
-            with torch.autocast("cuda", dtype=torch.float16):
-                loss = F.cross_entropy(model(x).flatten(0, 1).float(), y.flatten())
-            loss.backward()
-            runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
-    finally:
-        optimized_v3.KEEP_SPLIT_ATTENTION = saved
+    for keep in (False, True):
+        paths.configure(model, keep_split_attention=keep)
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = F.cross_entropy(model(x).flatten(0, 1).float(), y.flatten())
+        loss.backward()
+        runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
     assert torch.equal(runs[0][0], runs[1][0])
     for a, b in zip(runs[0][1], runs[1][1]):
         assert torch.equal(a, b)

@@ -14,12 +14,12 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from reconstruction_gate import check_case
+from reconstruction_gate import run_gate
 from reversability_amd import BaselineLM, ModelConfig, ReversibleLM, build_model
 from reversability_amd import optimized_v3 as v3
 from reversability_amd.kernels import FusedSwiGLU, enable_swiglu
 from reversability_amd.kernels_v3 import FusedRMSNorm
-from reversability_amd.optimized import ReusedMidpoint, chunked_backward, cpu_snapshot
+from reversability_amd.optimized import ReusedMidpoint, chunked_backward
 from reversability_amd.optimized_v3 import SplitMidpoint, TiledMLP, cached_head_backward, install_v3
 from reversability_amd.residual import midpoint_step
 from reversability_amd.reversible import forward_pair
@@ -60,15 +60,14 @@ def test_fused_paths_installed_on_cpu_model_refuse_to_run():
 @pytest.mark.parametrize("method", ["midpoint", "euler"])
 @pytest.mark.parametrize("precision", ["fp64", "fp32"])
 def test_reconstruction_gradients_and_update(method, precision):
-    report = check_case(method, precision, "cpu", 3, 17)
+    report = run_gate(method, precision, "cpu", 3, 17)
     if precision == "fp64":  # algebraic inverse: reconstruction exact to rounding
-        worst = max(v["max_abs"] for k, v in report["errors"].items() if k.startswith("state_"))
-        assert worst < 1e-13
+        assert report.worst_state_error() < 1e-13
 
 
 @pytest.mark.parametrize("core", ["reuse", "split"])
 def test_reconstruction_gate_with_optimized_core(core):
-    check_case("midpoint", "fp64", "cpu", 3, 17, prepare=lambda m: install_v3(m, core_mode=core))
+    run_gate("midpoint", "fp64", "cpu", 3, 17, prepare=lambda m: install_v3(m, core_mode=core))
 
 
 # ---------------------------------------------------------------------------
@@ -306,15 +305,6 @@ def test_chunked_tied_weight_gradients_masks_accumulation(method, dtype, chunk):
     for a, b in zip(original.parameters(), candidate.parameters()):
         torch.testing.assert_close(a.grad, b.grad, rtol=tolerance, atol=tolerance * .01)
     assert candidate.lm_head.weight is candidate.token_embedding.weight
-
-
-def test_cpu_snapshot_is_independent():
-    state = {"a": torch.ones(3), "b": [torch.zeros(2), (torch.arange(3),)], "c": 5}
-    snap = cpu_snapshot(state)
-    state["a"].add_(1)
-    state["b"][0].add_(1)
-    assert torch.equal(snap["a"], torch.ones(3)) and torch.equal(snap["b"][0], torch.zeros(2))
-    assert snap["c"] == 5
 
 
 # ---------------------------------------------------------------------------
