@@ -391,3 +391,71 @@ def test_mlp_output_unused_is_per_thread_and_gpu_only():
         worker.join()
         assert other == [0] and mlp._output_unused.depth == 1
     assert mlp._output_unused.depth == 0
+
+
+# ---------------------------------------------------------------------------
+# Path selection: per-model switches and the path record
+# ---------------------------------------------------------------------------
+
+def test_reconstruction_switches_are_per_model():
+    from reversability_amd import paths
+    a = build_model({"model": TINY, "method": "euler"})
+    b = build_model({"model": TINY, "method": "euler"})
+    assert paths.of(a.blocks) == paths.DEFAULT
+    paths.configure(a, fuse_euler_inverse=False)
+    assert not paths.of(a.blocks).fuse_euler_inverse
+    assert paths.of(b.blocks).fuse_euler_inverse  # the other model is untouched
+    assert not paths.of(copy.deepcopy(a).blocks).fuse_euler_inverse
+    c = build_model({"model": TINY, "method": "midpoint"})
+    off = paths.ReconstructionPaths(keep_split_attention=False)
+    install_v3(c, core_mode="split", paths=off)
+    assert paths.of(c.blocks) == off
+    assert install_v3(c, core_mode="split", paths=off) is c
+    with pytest.raises(ValueError):
+        install_v3(c, core_mode="split")  # another configuration: the default switches
+
+
+@pytest.mark.parametrize("switches", [dict(keep_split_attention=False),
+                                      dict(fuse_midpoint_norm=False), {}])
+def test_split_core_switches_keep_values_fp64(switches):
+    """Every switch setting gives the same fp64 loss and gradients on the CPU."""
+    from reversability_amd import paths
+    torch.manual_seed(5)
+    ref = build_model({"model": TINY, "method": "midpoint"}).double()
+    cand = copy.deepcopy(ref)
+    install_v3(cand, core_mode="split")
+    paths.configure(cand, **switches)
+    ids = torch.randint(31, (2, 8))
+    for model in (ref, cand):
+        F.cross_entropy(model(ids).flatten(0, 1), ids.flatten()).backward()
+    for p, q in zip(ref.parameters(), cand.parameters()):
+        torch.testing.assert_close(p.grad, q.grad, rtol=1e-10, atol=1e-12)
+
+
+def test_path_record_and_strict_mode():
+    from reversability_amd import paths
+    paths.reset()
+    paths.took("attention", "hip")
+    paths.took("attention", "hip")
+    paths.took("attention", "sdpa", "head size 48")
+    assert paths.report() == {"attention": {"hip": 2, "sdpa": 1}}
+    with paths.strict():
+        paths.took("attention", "hip")  # the HIP path never raises
+        with pytest.raises(paths.UnsupportedPathError, match="head size 48"):
+            paths.took("attention", "sdpa", "head size 48")
+    paths.took("attention", "sdpa", "outside strict() a fallback only counts")
+    assert paths.report()["attention"] == {"hip": 3, "sdpa": 2}
+    paths.reset()
+    assert paths.report() == {}
+
+
+def test_tiled_mlp_records_its_path_on_cpu():
+    from reversability_amd import paths
+    paths.reset()
+    x = torch.randn(2, 5, 8, dtype=torch.float64, requires_grad=True)
+    up = torch.randn(32, 8, dtype=torch.float64, requires_grad=True)
+    down = torch.randn(8, 16, dtype=torch.float64, requires_grad=True)
+    with paths.strict():  # the unfused CPU computation is what was asked for: no fallback
+        TiledMLP.apply(x, up, down, 3, False).sum().backward()
+    assert paths.report() == {"tiled_mlp": {"torch-gemm": 1}}
+    paths.reset()
