@@ -39,8 +39,16 @@ Also reported, on the same line:
                 same update launched eagerly beside it (``eager_*``).
   train_step_c5 configs[4]: the 12-layer Hamiltonian-Euler d1024 step on
                 the same kernels (reconstruction-stack core), tokens/s.
+  copy_ceiling  the same bytes moved by torch's own elementwise kernels (a
+                plain streaming kernel per config): mul (1 read, 1 write)
+                for RMSNorm fwd, add (2 reads, 1 write) for RMSNorm bwd and
+                SwiGLU fwd, mul over tensors of SwiGLU bwd's total bytes for
+                SwiGLU bwd; per kernel and for the whole step.
   cpu_baseline  the CPU oracle (oracle/kernels_ref.c, OpenMP) on the host's
-                cores: the same RMSNorm + SwiGLU step, in GB/s.
+                cores: the same RMSNorm + SwiGLU step, in GB/s.  The train
+                step carries its own: the reference's CPU training path
+                (fp32, reconstruction backward, AdamW) restated in
+                oracle/model_ref.py, on a bounded sample of configs[3].
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -190,6 +198,7 @@ def time_kernels(dev, steps: int, warmup: int):
         stop.record()
         torch.cuda.synchronize()
         per_kernel[name] = start.elapsed_time(stop) / steps  # ms
+    ceiling = copy_ceilings(dev, steps)
     # determinism spot check: relaunch the last sets, compare outputs bitwise
     r, w = step.set_for("rms_bwd", steps - 1), step.set_for("sw_bwd", steps - 1)
     step.run(steps - 1)
@@ -200,7 +209,46 @@ def time_kernels(dev, steps: int, warmup: int):
     if not (torch.equal(ref_dx, r["dx"]) and torch.equal(ref_du, w["du"])
             and torch.equal(ref_dw, r["dw"])):
         raise RuntimeError("kernel outputs are not run-to-run deterministic")
-    return wall / steps, per_kernel
+    return wall / steps, per_kernel, ceiling
+
+
+def copy_ceilings(dev, launches: int) -> dict:
+    """Average duration (ms) of torch's own elementwise kernels moving each
+    kernel's bytes, on rotating buffers (> 1.5 GB per shape), timed like the
+    kernels: RMSNorm fwd = mul [14848, 256] fp32 (1 read, 1 write); RMSNorm
+    bwd = add [14848, 256] fp32 (2 reads, 1 write); SwiGLU fwd = add
+    [14848, 1024] fp16 (2 reads, 1 write); SwiGLU bwd = mul [14848, 2560] fp16
+    (1 read, 1 write of 76 MB each: its 152 MB total)."""
+    import torch
+    shapes = {"rms_fwd": ((ROWS, D_MODEL), torch.float32, 1),
+              "rms_bwd": ((ROWS, D_MODEL), torch.float32, 2),
+              "sw_fwd": ((ROWS, D_FF), torch.float16, 2),
+              "sw_bwd": ((ROWS, 5 * D_FF // 2), torch.float16, 1)}
+    out = {}
+    for name, (shape, dtype, reads) in shapes.items():
+        one = shape[0] * shape[1] * torch.tensor([], dtype=dtype).element_size()
+        nsets = max(3, int(1.6e9 // ((reads + 1) * one)))
+        sets = [[torch.ones(shape, device=dev, dtype=dtype) for _ in range(reads + 1)]
+                for _ in range(nsets)]
+
+        def run(i, sets=sets, reads=reads):
+            t = sets[i % len(sets)]
+            if reads == 1:
+                torch.mul(t[0], 2.0, out=t[1])
+            else:
+                torch.add(t[0], t[1], out=t[2])
+        for i in range(max(20, 100)):
+            run(i)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(launches):
+            run(i)
+        stop.record()
+        torch.cuda.synchronize()
+        out[name] = start.elapsed_time(stop) / launches
+        del sets
+    torch.cuda.empty_cache()
+    return out
 
 
 def kernel_loop_only(dev, steps: int, warmup: int) -> None:
@@ -225,6 +273,18 @@ def kernel_loop_only(dev, steps: int, warmup: int) -> None:
           flush=True)
 
 
+def step_flop(model: dict, batch: int) -> int:
+    """Baseline-equivalent algorithmic FLOP of one training update: 6 per
+    token per matrix parameter (block projections and the tied head; forward
+    2, backward 4) plus the attention products, 3 x 4 T^2 d per sequence and
+    layer without the causal discount."""
+    d, f, layers = model["d_model"], model["d_ff"], model["n_layers"]
+    t, vocab = model["max_sequence_length"], model["vocab_size"]
+    block = layers * (3 * d * d + d * d + 2 * f * d + f * d)
+    tokens = batch * t
+    return 6 * tokens * (block + vocab * d) + 3 * layers * batch * 4 * t * t * d
+
+
 TRAIN_CONFIGS = {
     # configs[3]: midpoint 7 layers, d 256, split core, whole-batch MLP tile (MLP_TOKENS)
     "c4": {"model": {"vocab_size": 50257, "max_sequence_length": 512, "n_layers": 7,
@@ -237,6 +297,8 @@ TRAIN_CONFIGS = {
            "method": "euler", "step_size": 0.5, "batch": 16, "core_mode": "reference",
            "workload": "configs[4] euler 12L d1024 h16 ff4096 vocab50257"},
 }
+assert step_flop(TRAIN_CONFIGS["c4"]["model"], 33) == 2_234_411_384_832
+assert step_flop(TRAIN_CONFIGS["c5"]["model"], 16) == 59_596_093_784_064
 
 
 # Cached-head token chunk: the reference probes 1024 on a 16 GB T4
@@ -332,9 +394,13 @@ def train_step_bench(dev, steps: int, warmup: int, name: str = "c4", graph: bool
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) / steps, out
 
+    from reversability_amd import paths
     step, targets, cfg = make_train_step(dev, name)
     for _ in range(warmup):
         step()
+    paths.reset()  # which implementation each dispatching op took, over one update
+    step()
+    taken = paths.report()
     dt_eager, loss_eager = timed(step)
     loss_eager = float(loss_eager.item())
     dt, loss = dt_eager, loss_eager
@@ -346,7 +412,12 @@ def train_step_bench(dev, steps: int, warmup: int, name: str = "c4", graph: bool
         captured = CapturedStep(step, warmup)
         dt, out = timed(captured)
         loss = float(out.item())
+    flop = step_flop(cfg["model"], cfg["batch"])
     return {"tokens_per_s": targets / dt, "ms_per_step": dt * 1e3,
+            "algorithmic_flop_per_step": flop,
+            "TFLOPs": round(flop / dt / 1e12, 1),
+            "frac_of_mfma_peak": round(flop / dt / 1e12 / MFMA_PEAK_TFLOPS, 4),
+            "paths": taken,
             "launch": "HIP graph of the whole update, replayed" if graph else "eager",
             "eager_tokens_per_s": targets / dt_eager, "eager_ms_per_step": dt_eager * 1e3,
             "loss": loss / targets, "steps": steps, "warmup": warmup,
@@ -572,6 +643,58 @@ def cpu_baseline(seconds: float):
                       f"fwd+bwd) of oracle/kernels_ref.c with OpenMP, {dt:.1f} s"}
 
 
+def cpu_train_baseline(seconds: float, batch: int = 2):
+    """The reference's CPU training path -- fp32 (the reference disables
+    autocast on the CPU, src/reversibility/optimized.py:64-67), the
+    reconstruction backward, torch's AdamW (0.9, 0.95), wd 0.1 -- restated in
+    oracle/model_ref.py, on a bounded sample of configs[3]: ``batch`` of its
+    33 sequences per update (512 tokens each), updates repeated for about
+    ``seconds``; tokens/s on this host's cores."""
+    import numpy as np
+    import torch
+    from oracle import model_ref
+    from reversability_amd import build_model
+    threads = len(os.sched_getaffinity(0))
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    cfg = TRAIN_CONFIGS["c4"]
+    model, length = cfg["model"], cfg["model"]["max_sequence_length"]
+    torch.manual_seed(1337)
+    state = build_model({"model": model, "method": cfg["method"]}).state_dict()
+    params = {k: v for k, v in state.items() if k != "lm_head.weight"}
+    stream = np.random.default_rng(1337).integers(0, model["vocab_size"], batch * length + 1)
+    x = torch.from_numpy(stream[:-1].reshape(batch, length))
+    y = torch.from_numpy(stream[1:].reshape(batch, length))
+    leaves = {k: v.clone().requires_grad_(True) for k, v in params.items()}
+    opt = torch.optim.AdamW(leaves.values(), lr=6e-4, betas=(0.9, 0.95), weight_decay=0.1)
+
+    def update():
+        loss, grads = model_ref.loss_and_grads_reconstruct(
+            {k: v.detach() for k, v in leaves.items()}, x, y, model["n_layers"],
+            model["n_heads"], cfg["method"], cfg["step_size"])
+        for k, v in leaves.items():
+            v.grad = grads[k]
+        torch.nn.utils.clip_grad_norm_(leaves.values(), 1.0)
+        opt.step()
+        return loss
+
+    update()  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        update()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    torch.set_num_threads(saved)
+    per = dt / n
+    return {"value": round(batch * length / per, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port", "ms_per_step": round(per * 1e3, 1),
+            "sample": f"{n} updates of {batch} x {length} tokens of configs[3] (7L d256, vocab "
+                      f"50257): oracle/model_ref.py loss_and_grads_reconstruct in fp32, "
+                      f"clip 1.0, torch AdamW, {dt:.1f} s, torch.set_num_threads({threads})"}
+
+
 def load_traffic():
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
@@ -609,14 +732,18 @@ def main() -> int:
         print(json.dumps({"attention": attention_bench(dev), "embedding": embedding_bench(dev)}),
               flush=True)
         return 0
-    ms_step_s, per_kernel = time_kernels(dev, args.steps, args.warmup)
+    ms_step_s, per_kernel, ceiling = time_kernels(dev, args.steps, args.warmup)
     value = STEP_BYTES / ms_step_s / 1e9
     bytes_by = {"rms_fwd": RMS_FWD_BYTES, "rms_bwd": RMS_BWD_BYTES,
                 "sw_fwd": SW_FWD_BYTES, "sw_bwd": SW_BWD_BYTES}
-    kernels = {n: {"avg_us": per_kernel[n] * 1e3, "algorithmic_bytes": bytes_by[n],
-                   "GBps": bytes_by[n] / (per_kernel[n] * 1e-3) / 1e9,
-                   "frac_of_peak": bytes_by[n] / (per_kernel[n] * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    kernels = {n: {"avg_us": round(per_kernel[n] * 1e3, 2), "algorithmic_bytes": bytes_by[n],
+                   "GBps": round(bytes_by[n] / (per_kernel[n] * 1e-3) / 1e9, 1),
+                   "frac_of_peak": round(bytes_by[n] / (per_kernel[n] * 1e-3) / 1e9
+                                         / HBM_PEAK_GBS, 4),
+                   "copy_ceiling_us": round(ceiling[n] * 1e3, 2),
+                   "frac_of_copy_ceiling": round(ceiling[n] / per_kernel[n], 4)}
                for n in per_kernel}
+    ceiling_gbs = STEP_BYTES / (sum(ceiling.values()) * 1e-3) / 1e9
     achieved = kernels["sw_bwd"]["GBps"]
     line = {
         "metric": METRIC,
@@ -636,6 +763,12 @@ def main() -> int:
                    "buffer_sets": {"rmsnorm": RMS_SETS, "swiglu": SW_SETS},
                    "step_bytes": STEP_BYTES},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "copy_ceiling": {"GBps": round(ceiling_gbs, 1),
+                         "frac_of_peak": round(ceiling_gbs / HBM_PEAK_GBS, 4),
+                         "value_over_ceiling": round(value / ceiling_gbs, 4),
+                         "what": "the step's bytes moved by torch's elementwise mul/add "
+                                 "kernels of the same read/write shape, summed over the "
+                                 "four kernels (copy_ceiling_us per kernel)"},
         "roofline": {"bound": "hbm", "kernel": "swiglu_bwd_vec<fp16>",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
@@ -649,6 +782,8 @@ def main() -> int:
         line["embedding"] = embedding_bench(dev)
         line["train_step"] = train_step_bench(dev, args.train_steps, args.train_warmup)
         line["train_step_c5"] = train_step_bench(dev, 5, 2, "c5")
+        if args.cpu_seconds > 0:
+            line["train_step"]["cpu_baseline"] = cpu_train_baseline(args.cpu_seconds)
     if args.cpu_seconds > 0:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -13,6 +13,10 @@ computes (src/reversibility/reversible.py:95-97).
     midpoint step  src/reversibility/reversible.py:16-25  (p, q) -> (q, p + 2h f(q))
     euler step     src/reversibility/reversible.py:21-25  q' = q + A(p); p' = p + M(q')
     logits         src/reversibility/reversible.py:100-107 (tied head, final norm)
+    reconstruction src/reversibility/reversible.py:35-69 (the stack's backward:
+                   per layer, reversed, invert the step without a graph,
+                   recompute it with one and take its VJP) -- the reference's
+                   CPU training path, timed as the step's CPU baseline
 """
 from __future__ import annotations
 
@@ -100,4 +104,59 @@ def loss_and_grads(state, ids, labels, n_layers, n_heads, method, h=0.5, dtype=t
     loss = F.cross_entropy(out.flatten(0, 1), labels.cpu().flatten(), ignore_index=-100,
                            reduction=reduction)
     loss.backward()
+    return loss.detach(), {k: v.grad for k, v in params.items()}
+
+
+def _step(params, i, p, q, n_heads, method, h):
+    if method == "midpoint":
+        a = _A(params, i, q, n_heads)
+        return q, p + 2 * h * (a + _M(params, i, q + a))
+    q = q + _A(params, i, p, n_heads)
+    return p + _M(params, i, q), q
+
+
+def _inverse(params, i, p, q, n_heads, method, h):
+    if method == "midpoint":
+        a = _A(params, i, p, n_heads)
+        return q - 2 * h * (a + _M(params, i, p + a)), p
+    p0 = p - _M(params, i, q)
+    return p0, q - _A(params, i, p0, n_heads)
+
+
+def loss_and_grads_reconstruct(state, ids, labels, n_layers, n_heads, method, h=0.5,
+                               dtype=torch.float32, reduction="mean"):
+    """``loss_and_grads`` through the reconstruction backward: the stack runs
+    without a graph, the head and loss are differentiated at its final pair,
+    then each layer, last first, is inverted (no graph), recomputed with a
+    graph and differentiated with the pair's incoming gradients
+    (src/reversibility/reversible.py:35-69).  Midpoint and Euler only."""
+    if method not in ("midpoint", "euler"):
+        raise ValueError("reconstruction needs a reversible method")
+    params = {k: v.detach().to("cpu", dtype).clone().requires_grad_(True)
+              for k, v in state.items() if k != "lm_head.weight"}
+    ids, labels = ids.cpu(), labels.cpu()
+    t = ids.shape[1]
+    emb = params["token_embedding.weight"][ids] + params["position_embedding.weight"][:t]
+    with torch.no_grad():
+        p = q = emb.detach()
+        for i in range(n_layers):
+            p, q = _step(params, i, p, q, n_heads, method, h)
+    p, q = p.requires_grad_(True), q.requires_grad_(True)
+    head_in = q if method == "midpoint" else p
+    out = rms_norm(head_in, params["final_norm.weight"]) @ params["token_embedding.weight"].t()
+    loss = F.cross_entropy(out.flatten(0, 1), labels.flatten(), ignore_index=-100,
+                           reduction=reduction)
+    loss.backward()
+    dp = p.grad if p.grad is not None else torch.zeros_like(p)
+    dq = q.grad if q.grad is not None else torch.zeros_like(q)
+    p, q = p.detach(), q.detach()
+    for i in reversed(range(n_layers)):
+        with torch.no_grad():
+            p0, q0 = _inverse(params, i, p, q, n_heads, method, h)
+        p0, q0 = p0.requires_grad_(True), q0.requires_grad_(True)
+        np_, nq = _step(params, i, p0, q0, n_heads, method, h)
+        torch.autograd.backward((np_, nq), (dp, dq))
+        dp, dq = p0.grad, q0.grad
+        p, q = p0.detach(), q0.detach()
+    emb.backward(dp + dq)  # the boundary p = q = embedding
     return loss.detach(), {k: v.grad for k, v in params.items()}

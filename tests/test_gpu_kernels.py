@@ -537,3 +537,37 @@ def test_fused_norm_paths_with_unaligned_weight_take_the_unfused_path(cuda_devic
         passed, y2 = rms_norm_pass(leaf, norm)
         (passed.sum() + y2.float().sum()).backward()
     assert torch.isfinite(leaf.grad).all()
+
+
+@pytest.mark.parametrize("rows,width", [(1, 256), (15, 256), (17, 100), (255, 1020),
+                                        (257, 1024), (14848, 256), (32768, 1024), (4097, 1028),
+                                        (33, 66)])
+def test_rmsnorm_bwd_reduction_repeats(cuda_device, rows, width):
+    """The backward's fixed-order dweight reduction over its partial rows (one
+    to 256 of them, vector and scalar paths): dx and dw match the oracle, and
+    fifty calls on one workspace give the same bits."""
+    lib = _hip.library()
+    g = torch.Generator().manual_seed(rows * 7 + width)
+    x = torch.randn(rows, width, generator=g)
+    w = 1 + 0.02 * torch.randn(width, generator=g)
+    dy = torch.randn(rows, width, generator=g)
+    xd, wd, dyd = x.to(cuda_device), w.to(cuda_device), dy.to(cuda_device)
+    _, rstd = ops.rmsnorm_fwd(xd, wd, EPS32)
+    nbytes = lib.rv_rmsnorm_bwd_workspace_bytes(rows, width)
+    ws = torch.empty(nbytes // 4, device=cuda_device)
+    stream = _hip._stream(xd)
+    first = None
+    for i in range(50):
+        dx, dw = torch.empty_like(xd), torch.full_like(wd, float("nan"))
+        assert lib.rv_rmsnorm_bwd(xd.data_ptr(), wd.data_ptr(), dyd.data_ptr(), rstd.data_ptr(),
+                                  dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), nbytes, rows,
+                                  width, stream) == 0
+        if first is None:
+            first = (dx.clone(), dw.clone())
+        else:
+            assert torch.equal(dx, first[0]) and torch.equal(dw, first[1]), i
+    torch.cuda.synchronize()
+    odx, odw = oracle.rmsnorm_bwd(x.numpy(), w.numpy(), dy.numpy(), EPS32)
+    for got, ref in ((first[0], odx), (first[1], odw)):
+        err = np.abs(got.cpu().numpy().astype(np.float64) - ref).max() / np.abs(ref).max()
+        assert err <= 1e-5, err

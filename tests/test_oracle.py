@@ -366,3 +366,26 @@ def test_model_oracle_midpoint_is_exactly_invertible_fp64():
         # q is the previous step's reconstructed p: exact up to rounding
         torch.testing.assert_close(p, states[i][0], rtol=0, atol=1e-13)
         torch.testing.assert_close(q, states[i][1], rtol=0, atol=1e-13)
+
+
+@pytest.mark.parametrize("method", ["midpoint", "euler"])
+def test_model_ref_reconstruction_equals_autograd_fp64(method):
+    """The oracle's reconstruction backward (the reference's CPU training path,
+    timed as the step's CPU baseline) gives autograd's loss and gradients
+    through the unrolled recurrence in fp64."""
+    from oracle import model_ref
+    from reversability_amd import build_model
+    torch.manual_seed(3)
+    cfg = {"model": {"vocab_size": 61, "max_sequence_length": 16, "n_layers": 3, "n_heads": 2,
+                     "d_model": 16, "d_ff": 32}, "method": method, "step_size": 0.5}
+    state = build_model(cfg).state_dict()
+    ids = torch.randint(0, 61, (2, 16))
+    labels = ids.roll(-1, 1)
+    labels[:, -2:] = -100
+    want, grads = model_ref.loss_and_grads(state, ids, labels, 3, 2, method, dtype=torch.float64)
+    got, grads_r = model_ref.loss_and_grads_reconstruct(state, ids, labels, 3, 2, method,
+                                                        dtype=torch.float64)
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    assert set(grads) == set(grads_r)
+    for name in grads:
+        torch.testing.assert_close(grads_r[name], grads[name], rtol=1e-9, atol=1e-11, msg=name)
