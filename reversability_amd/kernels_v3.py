@@ -148,6 +148,13 @@ def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module, pre=None):
     return x, norm(x)
 
 
+def _fp16_norm_input(norm: torch.nn.Module, x: torch.Tensor) -> bool:
+    """Whether ``norm`` (routed by ``enable_rmsnorm(..., fp16_out=True)``) hands
+    its consumers the fp16 value of the fused kernels for this x."""
+    return (getattr(norm, "_rv_fp16_out", False) and x.is_cuda and x.dtype == torch.float32
+            and x.is_contiguous() and _fp16_out(x, norm.weight))
+
+
 def _sub_fusable(x: torch.Tensor, f: torch.Tensor, norm: torch.nn.Module) -> bool:
     """Whether rv_sub_rmsnorm_fwd_f16 gives what the fused fp16-output norm
     paths (rms_norm_pass / add_rms_norm) would compute after ``x - f``."""

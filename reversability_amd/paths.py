@@ -1,9 +1,10 @@
 """Path selection: per-model switches of the reconstruction backward and a
 record of which implementation each hot-path operation took.
 
-Switches (``ReconstructionPaths``).  The reconstruction backward has five
-optional restructurings, each leaving every value unchanged (the GPU tests
-compare each one on and off bit for bit).  They are settings of a model, kept
+Switches (``ReconstructionPaths``).  The reconstruction backward has six
+optional restructurings; the first five leave every value unchanged (the GPU
+tests compare each one on and off bit for bit), the sixth moves one
+linearisation point by a rounding (compared to fp32 truth).  They are settings of a model, kept
 on its ``blocks`` (the ``nn.ModuleList`` the stack Functions receive), so two
 models in one process can differ and nothing process-wide is mutated:
 
@@ -12,6 +13,12 @@ models in one process can differ and nothing process-wide is mutated:
     skip_unused_mlp_output  Euler VJP's rebuilt MLP output (graph-only) not computed
     keep_split_attention    split midpoint keeps the inversion's attention graph
     fuse_midpoint_norm      midpoint update made with the next layer's attention norm
+    euler_mlp_at_stored_q   Euler VJP reuses the inversion's M(q) graph, made at the
+                            stored state q (the point the forward evaluated M at)
+                            instead of at the rebuilt q0 + A(p0): one MLP evaluation
+                            per layer less; the linearisation point moves by the
+                            rounding of q0 + A(p0) (at most an ulp of fp32), so the
+                            gradients change within that rounding, not bit for bit
 
 ``configure(model, **flags)`` sets them; ``install_v3(..., paths=...)``
 records them at installation.  Models that never had them set use the
@@ -40,6 +47,7 @@ class ReconstructionPaths:
     skip_unused_mlp_output: bool = True
     keep_split_attention: bool = True
     fuse_midpoint_norm: bool = True
+    euler_mlp_at_stored_q: bool = True
 
 
 DEFAULT = ReconstructionPaths()

@@ -26,7 +26,9 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from . import paths
-from .kernels_v3 import add_rms_norm, inverse_add_rms_norm, inverse_rms_norm, rms_norm_pass
+from ._hip import ops
+from .kernels_v3 import (FusedAddRMSNorm, _fp16_norm_input, add_rms_norm, inverse_add_rms_norm,
+                         inverse_rms_norm, rms_norm_eps, rms_norm_pass)
 from .mlp import output_unused
 from .model import BaselineLM, Block, ModelConfig
 from .residual import eager_active, eager_updates, euler_step, midpoint_step
@@ -71,8 +73,73 @@ def inverse_pair(block, p, q, method, h):
 #   fuse_euler_inverse      the inversion's subtractions p - M(q) and q - A(p0)
 #       computed in the passes of the norms that read their results;
 #   skip_unused_mlp_output  the Euler VJP's rebuilt MLP output feeds only the
-#       graph-only next_p, so install_v3's tiled MLP does not compute it.
-# Each gives the same values as the plain inverse-then-recompute.
+#       graph-only next_p, so install_v3's tiled MLP does not compute it;
+#   euler_mlp_at_stored_q   the inversion's M(q) is made with its graph and
+#       serves the VJP (_euler_layer_vjp): M is linearised at the stored q,
+#       where the forward evaluated it, instead of at the rebuilt q0 + A(p0).
+# The first three give the same values as the plain inverse-then-recompute;
+# the last changes the gradients within the rounding of q0 + A(p0).
+
+
+def _grads_in_order(block, params, grads):
+    by_id = {id(w): g for w, g in zip(params, grads)}
+    return [by_id[id(w)] for w in block.parameters()]
+
+
+def _euler_layer_vjp(block, p, q, dp, dq, settings):
+    """Invert one Euler step -- (p, q) = (p0 + M(q), q0 + A(p0)) -- and take its
+    VJP with one evaluation of each force, both with their graphs: M at the
+    stored q (it inverts the step and, linearised there, serves the VJP) and
+    A at the recovered p0.  The VJP runs in two phases: the MLP's, giving the
+    gradient at M's input, then the step's rest (A, both norms and the
+    residual sums) with that gradient entering at the rebuilt q0 + A(p0).
+    Returns (p0, q0, dp0, dq0, parameter gradients in block.parameters()
+    order)."""
+    # the states may be the stack's own saved outputs: nothing here may extend
+    # their history (a graph reaching the stack node would re-enter its backward)
+    p, q = p.detach(), q.detach()
+    fused = _fp16_norm_input(block.mlp_norm, q)
+    with torch.enable_grad():
+        if fused:  # M's input is the fp16 norm of the stored q (graph from its leaf)
+            y_q, rstd_q = ops.rmsnorm_fwd(q, block.mlp_norm.weight.contiguous(),
+                                          rms_norm_eps(block.mlp_norm, q), True)
+            m_in = y_q.requires_grad_(True)
+            force = block.mlp(m_in)
+        else:  # M's input is the stored state itself
+            m_in = q.detach().requires_grad_(True)
+            force = block.mlp(block.mlp_norm(m_in))
+    with torch.no_grad():
+        if settings.fuse_euler_inverse:  # p0 and attn_norm(p0) in one pass
+            p0, pre_p0 = inverse_rms_norm(p, force.detach(), block.attn_norm)
+        else:
+            p0, pre_p0 = euler_step(p, force.detach(), -1), None
+    with torch.enable_grad():
+        p0 = p0.detach().requires_grad_(True)
+        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0)
+        attention = block.attn(normed_p0)
+    with torch.no_grad():
+        q0 = euler_step(q, attention.detach(), -1)
+    q0.requires_grad_(True)
+    mlp_params = tuple(block.mlp.parameters()) if fused else (*block.mlp_norm.parameters(),
+                                                              *block.mlp.parameters())
+    attn_params = (*block.attn_norm.parameters(), *block.attn.parameters())
+    with torch.enable_grad():
+        first = torch.autograd.grad(force, (m_in, *mlp_params), dp)
+        del force
+        if fused:  # next_q = q0 + A(p0) carrying the value q and its norm
+            next_q, y = FusedAddRMSNorm.apply(q0, attention, block.mlp_norm.weight,
+                                              rms_norm_eps(block.mlp_norm, q), (q, y_q, rstd_q))
+            norm_params = tuple(block.mlp_norm.parameters())
+            rest = torch.autograd.grad((next_q, y, p0_pass), (p0, q0, *attn_params, *norm_params),
+                                       (dq, first[0], dp))
+            grads = _grads_in_order(block, (*attn_params, *norm_params, *mlp_params),
+                                    (*rest[2:], *first[1:]))
+        else:  # next_q = q0 + A(p0), its gradient dq plus M's input gradient
+            next_q = euler_step(q0, attention, +1, graph_only=True)
+            rest = torch.autograd.grad((next_q, p0_pass), (p0, q0, *attn_params),
+                                       (dq + first[0], dp))
+            grads = _grads_in_order(block, (*attn_params, *mlp_params), (*rest[2:], *first[1:]))
+    return p0.detach(), q0.detach(), rest[0], rest[1], grads
 
 
 def _euler_inverse_for_vjp(block, p, q, settings):
@@ -130,6 +197,7 @@ class _InverseStack(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dp, dq):
         p, q, *_ = ctx.saved_tensors
+        p, q = p.detach(), q.detach()  # the forward's outputs: no history of this node
         grads: list = []
         settings = paths.of(ctx.blocks)
         # cache_enabled=False: torch <= 2.10 caches autocast weight casts made
@@ -139,6 +207,10 @@ class _InverseStack(torch.autograd.Function):
         with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype,
                             cache_enabled=False), eager_updates(ctx.eager):
             for block in reversed(ctx.blocks):
+                if ctx.method == "euler" and settings.euler_mlp_at_stored_q:
+                    p, q, dp, dq, layer = _euler_layer_vjp(block, p, q, dp, dq, settings)
+                    grads[0:0] = layer
+                    continue
                 if ctx.method == "euler" and settings.reuse_euler_attention:
                     next_p, next_q, p0, q0 = _euler_inverse_for_vjp(block, p, q, settings)
                 else:

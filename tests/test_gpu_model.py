@@ -416,7 +416,7 @@ def test_euler_attention_reuse_bitwise(cuda_device):
     ids = torch.randint(0, 512, (2, 256), device=cuda_device)
     runs = []
     for reuse in (False, True):
-        paths.configure(model, reuse_euler_attention=reuse)
+        paths.configure(model, reuse_euler_attention=reuse, euler_mlp_at_stored_q=False)
         model.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.float16):
             loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
@@ -445,7 +445,7 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch
     ids = torch.randint(0, 512, (2, 256), device=cuda_device)
     runs = []
     for on in (False, True):
-        paths.configure(model, **{switch: on})
+        paths.configure(model, **{switch: on}, euler_mlp_at_stored_q=False)
         model.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.float16):
             loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
@@ -536,3 +536,41 @@ def test_captured_train_step_matches_eager_bitwise(cuda_device, config):
         assert torch.equal(eager.scaler._scale, graphed.scaler._scale)
     changed = sum(not torch.equal(b, p) for b, p in zip(before, graphed.model.parameters()))
     assert changed == len(before)
+
+
+def test_euler_mlp_at_stored_state_within_truth(cuda_device):
+    """The Euler VJP with M linearised at the stored q (euler_mlp_at_stored_q,
+    one MLP evaluation per layer less) against the rebuild at q0 + A(p0): the
+    same loss bit for bit (the forward is unchanged) and gradients no farther
+    from the fp32 truth than the rebuild's, within 1.25x per parameter (floor
+    1e-2 relative L2)."""
+    from reversability_amd.residual import eager_updates
+    torch.manual_seed(19)
+    cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 4, "n_heads": 4,
+                     "d_model": 256, "d_ff": 512}, "method": "euler", "step_size": 0.5}
+    base = build_model(cfg).to(cuda_device)
+    ids = torch.randint(0, 512, (4, 256), device=cuda_device)
+    truth = copy.deepcopy(base)
+    truth.backward_mode = "autograd"
+    with eager_updates():
+        F.cross_entropy(truth(ids).flatten(0, 1), ids.flatten()).backward()
+    model = copy.deepcopy(base)
+    install_v3(model, core_mode="reference", mlp_tokens=1024, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
+    enable_linear(model)
+    enable_attention(model)
+    runs = {}
+    for on in (False, True):
+        paths.configure(model, euler_mlp_at_stored_q=on)
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+        loss.backward()
+        runs[on] = (loss.detach(), {n: p.grad.clone() for n, p in model.named_parameters()})
+    assert torch.equal(runs[False][0], runs[True][0])
+    worst = 0.0
+    for name, p in truth.named_parameters():
+        stored, rebuilt = rel_l2(runs[True][1][name], p.grad), rel_l2(runs[False][1][name], p.grad)
+        worst = max(worst, stored)
+        assert stored <= max(1e-2, 1.25 * rebuilt), (name, stored, rebuilt)
+    print(f"\n[euler stored-q] worst gradient relative L2 to the fp32 truth {worst:.3e}", flush=True)
