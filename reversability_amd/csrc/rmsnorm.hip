@@ -756,12 +756,19 @@ static __device__ __align__(256) float scratch[kNoallocScratchFloats];
 namespace {
 
 // The current device's address of `scratch` (queried on its first use on that
-// device), or an rv_status.
-int scratch_address(float** out) {
+// device), or an rv_status.  A stream of another device is refused: the
+// kernels would run there with this device's address.
+int scratch_address(hipStream_t stream, float** out) {
   int dev = 0;
   const hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return rv_host::hip_fail(e);
   if (dev < 0 || dev >= kMaxScratchDevices) return RV_ERR_UNSUPPORTED;
+  if (stream != nullptr) {
+    int sdev = -1;
+    const hipError_t es = hipStreamGetDevice(stream, &sdev);
+    if (es != hipSuccess) return rv_host::hip_fail(es);
+    if (sdev != dev) return RV_ERR_UNSUPPORTED;
+  }
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_ptr[dev] == nullptr) {
     void* ptr = nullptr;
@@ -870,7 +877,7 @@ int rv_rmsnorm_bwd_noalloc(const float* x, const float* w, const float* dy, cons
   const int64_t need = (int64_t)plan_bwd(rows).nparts * width * (int64_t)sizeof(float);
   if (need > kNoallocScratchFloats * (int64_t)sizeof(float)) return RV_ERR_WORKSPACE;
   float* ws = nullptr;
-  const int st = scratch_address(&ws);
+  const int st = scratch_address((hipStream_t)stream, &ws);
   if (st != RV_OK) return st;
   // The partial rows are written in full before the reduce reads them, so the
   // previous call's contents need no clearing.

@@ -79,3 +79,21 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(cuda_device):
     assert lib.rv_rmsnorm_bwd_noalloc(ctypes.c_void_p(x.data_ptr()), w.data_ptr(), x.data_ptr(),
                                       rstd.data_ptr(), x.data_ptr(), w.data_ptr(), 0, 256,
                                       None) == 2
+
+
+@pytest.mark.gpu
+def test_noalloc_on_a_stream_of_the_current_device(cuda_device):
+    """A non-default stream of the current device is accepted (the entry point
+    checks the stream's device against the current one) and gives the same bits."""
+    lib = _hip.library()
+    x, w, dy, rstd = _inputs(2048, 256, 7, cuda_device)
+    ref_dx, ref_dw = _with_workspace(lib, x, w, dy, rstd)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=cuda_device)
+    dx = torch.full_like(x, float("nan"))
+    dw = torch.full_like(w, float("nan"))
+    st = lib.rv_rmsnorm_bwd_noalloc(x.data_ptr(), w.data_ptr(), dy.data_ptr(), rstd.data_ptr(),
+                                    dx.data_ptr(), dw.data_ptr(), 2048, 256, side.cuda_stream)
+    assert st == 0, lib.rv_status_string(st)
+    side.synchronize()
+    assert torch.equal(dx, ref_dx) and torch.equal(dw, ref_dw)
