@@ -1,10 +1,11 @@
 // Fused RMSNorm forward/backward for gfx950.
 //
 // Layout: x, y, dy, dx are [rows, width] FP32 row-major; w and dw are
-// [width]; rstd is [rows].  One wavefront owns one row at a time: with
-// width = 256 each of the 64 lanes holds one float4 (16-byte loads, the whole
-// row is one 1 KiB coalesced access); wider rows use VEC float4 per lane.
-// Each wave keeps RPW rows in flight to cover HBM latency.
+// [width]; rstd is [rows].  A row belongs to a group of G lanes of one wave
+// (G = 16 for width <= 256: four rows per wave, each lane holding VEC float4
+// of its row at float4 indices v*16 + lane%16, so one load instruction reads
+// four 256-byte row segments; G = 64 for wider rows: one row per wave, VEC
+// float4 per lane).  The row sums are DPP reductions inside the group.
 //
 // Backward is a single pass over x and dy: every wave computes dx for its
 // rows and accumulates dy * (x * rstd) per column in registers; the waves of
@@ -35,15 +36,19 @@ using rv::wave_sum;
 
 // Launch shapes chosen by timing sweeps on MI355X at the configs' shapes
 // (x [14848, 256] fp32), over > 1.5 GB of rotating buffers:
-//   forward   8 blocks of 4 waves per CU, one row per wave in flight
-//   backward  256 blocks of 16 waves, ~58 rows per block
-// Loads of x / dy are plain (they are often still in the Infinity Cache
-// when RMSNorm runs inside a model step); stores of y / dx are streaming.
+//   forward, width <= 256  16 lanes per row, one group of four rows per
+//                          wave, a grid that covers every row (no loop):
+//                          every load is in flight at once (C1: 7.6 -> 6.1 us
+//                          against the one-row-per-wave persistent grid)
+//   forward, wider rows    8 blocks of 4 waves per CU, persistent, one row per
+//                          wave in flight
+//   backward, width <= 256 the same layout, blocks of 4 waves x 4 .. 8 four-row
+//                          groups (C1: 232 blocks of 64 rows), every row of a
+//                          block in flight at once (13.1 -> 11.9 us)
+//   backward, wider rows   256 blocks of 4 .. 16 waves, ~128 rows per block
+// Stores of y / dx are streaming.
 #ifndef RV_RMS_FWD_BLOCKS_PER_CU
 #define RV_RMS_FWD_BLOCKS_PER_CU 8
-#endif
-#ifndef RV_RMS_FWD_RPW
-#define RV_RMS_FWD_RPW 1
 #endif
 #ifndef RV_RMS_BWD_WAVES
 #define RV_RMS_BWD_WAVES 16
@@ -54,7 +59,7 @@ using rv::wave_sum;
 
 
 constexpr int kFwdWaves = 4;                 // waves per block, forward
-constexpr int kBwdWaves = RV_RMS_BWD_WAVES;  // waves per block, backward (width <= 512)
+constexpr int kBwdWaves = RV_RMS_BWD_WAVES;  // waves per block, backward (scalar path, width <= 512)
 // Waves per backward block by vector count per lane (width <= 256 * VEC):
 // 2 rows x (x, dy) x VEC float4 per register tile, two tiles in flight.
 constexpr int bwd_waves(int vec) { return vec <= 2 ? kBwdWaves : (vec == 4 ? 8 : 4); }
@@ -68,13 +73,14 @@ constexpr int kMaxVec = 16;      // float4 per lane => width <= 4096
 constexpr int kMaxEpl = 64;      // scalar path: elements per lane <= 64
 
 // ---------------------------------------------------------------------------
-// Forward, width % 4 == 0, width <= 256 * VEC.  Persistent: wave w of the
-// grid handles row groups w, w + W, w + 2W, ... (W = waves in the grid; a
-// group is RPW consecutive rows) and alternates between two register tiles,
-// issuing the next group's loads before reducing the current one.  Rows past
-// the end are clamped to the last row for loading (one cached line, no
-// branch) and never stored.  With ADD the row input is x + float(f) (fused
-// residual add) and that sum is also written to h.
+// Forward, width % 4 == 0, width <= 4 * G * VEC.  A wave handles groups of
+// 64/G consecutive rows (lane l works on row group_first + l/G).  Persistent
+// (rms_fwd_vec): wave w of the grid handles groups w, w + W, w + 2W, ...
+// (W = waves in the grid) and alternates between two register tiles, issuing
+// the next group's loads before reducing the current one.  Rows past the end
+// are clamped to the last row for loading (one cached line, no branch) and
+// never stored.  With ADD the row input is
+// x + float(f) (fused residual add) and that sum is also written to h.
 // ---------------------------------------------------------------------------
 // Four normalized values to y (fp32: one streaming 16-byte store; fp16:
 // rounded to nearest even, one streaming 8-byte store).  The fp16 values are
@@ -92,30 +98,35 @@ __device__ __forceinline__ void store_y(__half* p, float4 v) {
   __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(p));
 }
 
+// Lane l's first column of its row's float4 number v (G lanes per row).
+template <int G>
+__device__ __forceinline__ int lane_col(int v, int lane) {
+  return (v * G + (lane & (G - 1))) * 4;
+}
+
 // TWO: a second force operand g (the midpoint update's M(...) beside f = A(...)).
-template <int VEC, int RPW, typename F, bool ADD, bool TWO = false>
+template <int VEC, typename F, bool ADD, bool TWO = false>
 struct RowTile {
-  float4 x[RPW][VEC];
-  float4 f[ADD ? RPW : 1][VEC];
-  float4 g[TWO ? RPW : 1][TWO ? VEC : 1];
+  float4 x[VEC];
+  float4 f[ADD ? VEC : 1];
+  float4 g[TWO ? VEC : 1];
 };
 
-template <int VEC, int RPW, typename F, bool ADD, bool TWO>
-__device__ __forceinline__ void rms_load(RowTile<VEC, RPW, F, ADD, TWO>& t,
+// FULL: width == 4 * G * VEC (no column clamp).
+template <int VEC, int G, bool FULL = false, typename F, bool ADD, bool TWO>
+__device__ __forceinline__ void rms_load(RowTile<VEC, F, ADD, TWO>& t,
                                          const float* __restrict__ x, const F* __restrict__ f,
                                          int64_t row0, int64_t rows, int width, int lane,
                                          const F* __restrict__ g = nullptr) {
+  const int64_t r = row0 + lane / G;
+  const int64_t row = r < rows ? r : rows - 1;
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const int col = (v * 64 + lane) * 4;
-      const int col_c = col < width ? col : width - 4;
-      t.x[r][v] = rv::ld_f4(x + row * width + col_c);
-      if constexpr (ADD) t.f[r][v] = rv::load4f(f + row * width + col_c);
-      if constexpr (TWO) t.g[r][v] = rv::load4f(g + row * width + col_c);
-    }
+  for (int v = 0; v < VEC; ++v) {
+    const int col = lane_col<G>(v, lane);
+    const int col_c = FULL || col < width ? col : width - 4;
+    t.x[v] = rv::ld_f4(x + row * width + col_c);
+    if constexpr (ADD) t.f[v] = rv::load4f(f + row * width + col_c);
+    if constexpr (TWO) t.g[v] = rv::load4f(g + row * width + col_c);
   }
 }
 
@@ -135,83 +146,137 @@ __device__ __forceinline__ float midpoint_elem(float x, float a, float m, float 
 // is stored and the row input is d + f; 3 -- it is the midpoint update of x
 // with the force terms f and g (midpoint_elem).  The row input is stored in h
 // for every SUBM but 0 without h.
-template <int VEC, int RPW, typename F, bool ADD, typename Y, int SUBM = 0>
-__device__ __forceinline__ void rms_finish(RowTile<VEC, RPW, F, ADD, SUBM == 3>& t,
+// FULL: width == 4 * G * VEC (every lane's columns exist: no column masks, and
+// the stores sit under the row predicate alone).
+template <int VEC, int G, typename F, bool ADD, typename Y, int SUBM = 0, bool FULL = false>
+__device__ __forceinline__ void rms_finish(RowTile<VEC, F, ADD, SUBM == 3>& t,
                                            const float4 (&wv)[VEC],
                                            float* __restrict__ h, Y* __restrict__ y,
                                            float* __restrict__ rstd, int64_t row0, int64_t rows,
                                            int width, float eps, int lane,
                                            float* __restrict__ d = nullptr, float scale = 0.f,
                                            int sign = 1) {
+  const int64_t row = row0 + lane / G;
+  float ss = 0.f;
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const int64_t row = row0 + r;
-    float ss = 0.f;
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      const bool ok = (v * 64 + lane) * 4 < width;
-      if constexpr (ADD && SUBM == 0) {
-        t.x[r][v].x = t.x[r][v].x + t.f[r][v].x;
-        t.x[r][v].y = t.x[r][v].y + t.f[r][v].y;
-        t.x[r][v].z = t.x[r][v].z + t.f[r][v].z;
-        t.x[r][v].w = t.x[r][v].w + t.f[r][v].w;
-      } else if constexpr (ADD && SUBM == 3) {
-        t.x[r][v].x = midpoint_elem(t.x[r][v].x, t.f[r][v].x, t.g[r][v].x, scale, sign);
-        t.x[r][v].y = midpoint_elem(t.x[r][v].y, t.f[r][v].y, t.g[r][v].y, scale, sign);
-        t.x[r][v].z = midpoint_elem(t.x[r][v].z, t.f[r][v].z, t.g[r][v].z, scale, sign);
-        t.x[r][v].w = midpoint_elem(t.x[r][v].w, t.f[r][v].w, t.g[r][v].w, scale, sign);
-      } else if constexpr (ADD) {
-        t.x[r][v].x = t.x[r][v].x - t.f[r][v].x;
-        t.x[r][v].y = t.x[r][v].y - t.f[r][v].y;
-        t.x[r][v].z = t.x[r][v].z - t.f[r][v].z;
-        t.x[r][v].w = t.x[r][v].w - t.f[r][v].w;
-        if constexpr (SUBM == 2) {
-          if (row < rows && ok) rv::st_f4s(d + row * width + (v * 64 + lane) * 4, t.x[r][v]);
-          t.x[r][v].x = t.x[r][v].x + t.f[r][v].x;
-          t.x[r][v].y = t.x[r][v].y + t.f[r][v].y;
-          t.x[r][v].z = t.x[r][v].z + t.f[r][v].z;
-          t.x[r][v].w = t.x[r][v].w + t.f[r][v].w;
-        }
+  for (int v = 0; v < VEC; ++v) {
+    const bool ok = FULL || lane_col<G>(v, lane) < width;
+    if constexpr (ADD && SUBM == 0) {
+      t.x[v].x = t.x[v].x + t.f[v].x;
+      t.x[v].y = t.x[v].y + t.f[v].y;
+      t.x[v].z = t.x[v].z + t.f[v].z;
+      t.x[v].w = t.x[v].w + t.f[v].w;
+    } else if constexpr (ADD && SUBM == 3) {
+      t.x[v].x = midpoint_elem(t.x[v].x, t.f[v].x, t.g[v].x, scale, sign);
+      t.x[v].y = midpoint_elem(t.x[v].y, t.f[v].y, t.g[v].y, scale, sign);
+      t.x[v].z = midpoint_elem(t.x[v].z, t.f[v].z, t.g[v].z, scale, sign);
+      t.x[v].w = midpoint_elem(t.x[v].w, t.f[v].w, t.g[v].w, scale, sign);
+    } else if constexpr (ADD) {
+      t.x[v].x = t.x[v].x - t.f[v].x;
+      t.x[v].y = t.x[v].y - t.f[v].y;
+      t.x[v].z = t.x[v].z - t.f[v].z;
+      t.x[v].w = t.x[v].w - t.f[v].w;
+      if constexpr (SUBM == 2) {
+        if (row < rows && ok) rv::st_f4s(d + row * width + lane_col<G>(v, lane), t.x[v]);
+        t.x[v].x = t.x[v].x + t.f[v].x;
+        t.x[v].y = t.x[v].y + t.f[v].y;
+        t.x[v].z = t.x[v].z + t.f[v].z;
+        t.x[v].w = t.x[v].w + t.f[v].w;
       }
-      const float4 q = rv::keep_if(t.x[r][v], ok);
-      ss = ss + q.x * q.x;
-      ss = ss + q.y * q.y;
-      ss = ss + q.z * q.z;
-      ss = ss + q.w * q.w;
     }
-    ss = wave_sum(ss);
-    const float rs = rsqrtf(ss / (float)width + eps);
-    if (row < rows) {
+    const float4 q = rv::keep_if(t.x[v], ok);
+    ss = ss + q.x * q.x;
+    ss = ss + q.y * q.y;
+    ss = ss + q.z * q.z;
+    ss = ss + q.w * q.w;
+  }
+  ss = rv::group_sum<G>(ss);
+  const float rs = rsqrtf(ss / (float)width + eps);
+  float4 o[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const float4 q = t.x[v];
+    o[v].x = (q.x * rs) * wv[v].x;
+    o[v].y = (q.y * rs) * wv[v].y;
+    o[v].z = (q.z * rs) * wv[v].z;
+    o[v].w = (q.w * rs) * wv[v].w;
+  }
+  const bool row_ok = row < rows;
+  if constexpr (FULL) {
+    if (row_ok) {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        const int col = (v * 64 + lane) * 4;
-        if (col < width) {
-          const float4 q = t.x[r][v];
-          float4 o;
-          o.x = (q.x * rs) * wv[v].x;
-          o.y = (q.y * rs) * wv[v].y;
-          o.z = (q.z * rs) * wv[v].z;
-          o.w = (q.w * rs) * wv[v].w;
-          store_y(y + row * width + col, o);
-          if constexpr (ADD) rv::st_f4s(h + row * width + col, q);
-        }
+        const int col = lane_col<G>(v, lane);
+        store_y(y + row * width + col, o[v]);
+        if constexpr (ADD) rv::st_f4s(h + row * width + col, t.x[v]);
       }
-      if (lane == 0) rstd[row] = rs;
+      if ((lane & (G - 1)) == 0) rstd[row] = rs;
     }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int col = lane_col<G>(v, lane);
+      if (row_ok && col < width) {
+        store_y(y + row * width + col, o[v]);
+        if constexpr (ADD) rv::st_f4s(h + row * width + col, t.x[v]);
+      }
+    }
+    if (row_ok && (lane & (G - 1)) == 0) rstd[row] = rs;
   }
 }
 
-template <int VEC, int RPW, typename F, bool ADD, typename Y, int SUBM = 0>
+// One four-row group per wave, 16 lanes per row (width <= 256), no loop: the
+// grid covers every row and each wave's row loads are its first memory
+// instructions, so every row load of the launch is in flight at once.
+// FULL (width = 64 VEC): the weight loads follow the row sum (the compiler
+// places them in the store branch): 3712 waves loading the same 1 KiB of w
+// together with their rows made every wave wait on those few L2 lines (C1:
+// 7.15 us with w loaded beside x, 6.84 staged once per block through LDS, 6.3
+// after the row sum).  Other widths keep w beside x: an empty asm consumes it
+// there, or the compiler would sink each column's weight load into that
+// column's store branch, one round trip after another.
+template <int VEC, bool FULL, typename F, bool ADD, typename Y, int SUBM = 0>
+__global__ __launch_bounds__(kFwdWaves * 64)
+void rms_fwd_grp(const float* __restrict__ x, const F* __restrict__ f,
+                 const float* __restrict__ w, float* __restrict__ h,
+                 Y* __restrict__ y, float* __restrict__ rstd,
+                 int64_t rows, int width, float eps, float* __restrict__ d = nullptr,
+                 const F* __restrict__ g = nullptr, float scale = 0.f, int sign = 1) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6)) * 4;
+  if (row0 >= rows) return;  // wave-uniform
+  RowTile<VEC, F, ADD, SUBM == 3> a;
+  rms_load<VEC, 16, FULL>(a, x, f, row0, rows, width, lane, g);
+  // the row loads all issued before the row sum starts waiting on them
+  __builtin_amdgcn_sched_barrier(0);
+  float4 wv[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    const int col = lane_col<16>(v, lane);
+    wv[v] = rv::ld_f4(w + (FULL ? col : (col < width ? col : width - 4)));
+  }
+  if constexpr (!FULL) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      asm volatile("" ::"v"(wv[v].x), "v"(wv[v].y), "v"(wv[v].z), "v"(wv[v].w));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  rms_finish<VEC, 16, F, ADD, Y, SUBM, FULL>(a, wv, h, y, rstd, row0, rows, width, eps, lane,
+                                             d, scale, sign);
+}
+
+template <int VEC, int G, typename F, bool ADD, typename Y, int SUBM = 0>
 __global__ __launch_bounds__(kFwdWaves * 64)
 void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
                  const float* __restrict__ w, float* __restrict__ h,
                  Y* __restrict__ y, float* __restrict__ rstd,
                  int64_t rows, int width, float eps, float* __restrict__ d = nullptr,
                  const F* __restrict__ g = nullptr, float scale = 0.f, int sign = 1) {
+  constexpr int RW = 64 / G;  // rows per wave group
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * kFwdWaves;
   const int64_t wave = (int64_t)blockIdx.x * kFwdWaves + (threadIdx.x >> 6);
-  const int64_t groups = (rows + RPW - 1) / RPW;
+  const int64_t groups = (rows + RW - 1) / RW;
   if (wave >= groups) return;  // wave-uniform
   const int64_t iters = (groups - 1 - wave) / nwaves + 1;
 
@@ -219,22 +284,22 @@ void rms_fwd_vec(const float* __restrict__ x, const F* __restrict__ f,
   float4 wv[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) {
-    const int col = (v * 64 + lane) * 4;
+    const int col = lane_col<G>(v, lane);
     wv[v] = rv::ld_f4(w + (col < width ? col : width - 4));
   }
-  const int64_t stride = nwaves * RPW;
-  int64_t row0 = wave * RPW;
-  RowTile<VEC, RPW, F, ADD, SUBM == 3> a, b;
-  rms_load(a, x, f, row0, rows, width, lane, g);
+  const int64_t stride = nwaves * RW;
+  int64_t row0 = wave * RW;
+  RowTile<VEC, F, ADD, SUBM == 3> a, b;
+  rms_load<VEC, G>(a, x, f, row0, rows, width, lane, g);
   for (int64_t k = 0; k < iters; k += 2) {
-    rms_load(b, x, f, row0 + stride, rows, width, lane, g);
-    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(a, wv, h, y, rstd, row0, rows, width, eps, lane, d,
-                                          scale, sign);
+    rms_load<VEC, G>(b, x, f, row0 + stride, rows, width, lane, g);
+    rms_finish<VEC, G, F, ADD, Y, SUBM>(a, wv, h, y, rstd, row0, rows, width, eps, lane, d,
+                                        scale, sign);
     if (k + 1 >= iters) break;
     row0 += stride;
-    rms_load(a, x, f, row0 + stride, rows, width, lane, g);
-    rms_finish<VEC, RPW, F, ADD, Y, SUBM>(b, wv, h, y, rstd, row0, rows, width, eps, lane, d,
-                                          scale, sign);
+    rms_load<VEC, G>(a, x, f, row0 + stride, rows, width, lane, g);
+    rms_finish<VEC, G, F, ADD, Y, SUBM>(b, wv, h, y, rstd, row0, rows, width, eps, lane, d,
+                                        scale, sign);
     row0 += stride;
   }
 }
@@ -452,6 +517,200 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
 }
 
 // ---------------------------------------------------------------------------
+// Backward, width % 4 == 0 and width <= 256: the forward's 16-lanes-per-row
+// layout (four rows per wave, lane l on row l/16 of its group, float4 number
+// v*16 + l%16 of the row).  Block b owns rows [b*R, min((b+1)*R, rows)),
+// R = 16 NG; its 4 NG four-row groups are dealt to the four waves
+// round-robin, and each wave issues the loads of its NG groups before
+// finishing any of them: every row of the block is in flight at once.  NG
+// (4 .. 8) is the fewest that keep the grid at one block per compute unit
+// (256 blocks; C1: 232 blocks of 64 rows), so no compute unit streams two
+// blocks' rows while others idle.  dweight per column: each lane sums its
+// own rows in order, then the block sums (wave, row-in-group) in order
+// through LDS and writes one contiguous partial row.
+// ---------------------------------------------------------------------------
+template <int VEC, bool ACC, bool PASS>
+struct GrpTile {
+  float4 x[VEC], g[VEC];
+  float4 h[ACC ? VEC : 1];
+  float4 p[PASS ? VEC : 1];
+  float rs;
+};
+
+constexpr int kGrpWaves = 4;    // waves per block
+constexpr int kGrpMinLoads = 4;  // four-row groups in flight per wave: 4 .. 8,
+constexpr int kGrpMaxLoads = 8;  // the fewest that keep the grid at <= 256 blocks
+
+// Loads of group k of the block: rows base + (k * kGrpWaves + wave) * 4 + lane/16,
+// clamped to end - 1; addresses are block-uniform base pointers plus 32-bit
+// lane offsets (a block's 16 NG rows).
+template <int VEC, int NG, bool FULL, typename G, bool ACC, bool PASS>
+__device__ __forceinline__ void grp_load(GrpTile<VEC, ACC, PASS> (&t)[NG],
+                                         const float* __restrict__ x, const G* __restrict__ dy,
+                                         const float* __restrict__ rstd,
+                                         const float* __restrict__ dh,
+                                         const float* __restrict__ dpass, int64_t base,
+                                         int64_t end, int width, int wave, int lane) {
+  const int nrows = (int)(end - base);  // 1 .. 16 NG
+  const float* xb = x + base * width;
+  const G* gb = dy + base * width;
+  const float* hb = ACC ? dh + base * width : nullptr;
+  const float* pb = PASS ? dpass + base * width : nullptr;
+#pragma unroll
+  for (int k = 0; k < NG; ++k) {
+    const int r = (k * kGrpWaves + wave) * 4 + (lane >> 4);
+    const int rc = r < nrows ? r : nrows - 1;  // clamped, valid
+    t[k].rs = rstd[base + rc];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      const int col = lane_col<16>(v, lane);
+      const unsigned off = (unsigned)(rc * width + (FULL || col < width ? col : width - 4));
+      t[k].x[v] = rv::ld_f4(xb + off);
+      t[k].g[v] = rv::load4f(gb + off);
+      if constexpr (ACC) t[k].h[v] = rv::ld_f4(hb + off);
+      if constexpr (PASS) t[k].p[v] = rv::ld_f4(pb + off);
+    }
+  }
+}
+
+template <int VEC, int NG, bool FULL, typename G, bool ACC, bool H16, bool PASS>
+__global__ __launch_bounds__(kGrpWaves * 64)
+void rms_bwd_grp(const float* __restrict__ x, const float* __restrict__ w,
+                 const G* __restrict__ dy, const float* __restrict__ rstd,
+                 float* __restrict__ dx, float* __restrict__ partial,
+                 int64_t rows, int width,
+                 const float* __restrict__ dh = nullptr, __half* __restrict__ dx16 = nullptr,
+                 const float* __restrict__ dpass = nullptr) {
+  constexpr int GL = 16;  // lanes per row
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane >> 4;
+  constexpr int kRows = kGrpWaves * NG * 4;  // rows per block
+  const int64_t start = (int64_t)blockIdx.x * kRows;
+  const int64_t end = start + kRows < rows ? start + kRows : rows;
+  const float fwidth = (float)width;
+
+  // The weight is staged once per block through LDS: wave 0 loads it ahead of
+  // its row loads (a few L2 lines that every block reads: loaded by every wave
+  // beside its rows they held each wave's first wait), every wave then issues
+  // all of its row loads, and the block meets at one barrier before the row
+  // math (w of a column >= width only meets masked values).
+  __shared__ float4 wlds[VEC * GL];
+  float4 wr[VEC];
+  if (wave == 0) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (v * 64 + lane < VEC * GL) {
+        const int col = (v * 64 + lane) * 4;
+        wr[v] = rv::ld_f4(w + (FULL || col < width ? col : width - 4));
+      }
+  }
+  GrpTile<VEC, ACC, PASS> t[NG];
+  grp_load<VEC, NG, FULL, G, ACC, PASS>(t, x, dy, rstd, dh, dpass, start, end, width, wave,
+                                        lane);
+  // every row load issued before the first wait (the scheduler would otherwise
+  // interleave the first group's math, and its waits, with the later loads)
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (v * 64 + lane < VEC * GL) wlds[v * 64 + lane] = wr[v];
+  }
+  __syncthreads();
+  float4 wv[VEC], acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    wv[v] = wlds[v * GL + (lane & (GL - 1))];
+    acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  {
+    const int nrows = (int)(end - start);  // 1 .. kRows
+    float* dxb = dx + start * width;
+    __half* d16b = H16 ? dx16 + start * width : nullptr;
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+      const int r = (k * kGrpWaves + wave) * 4 + sub;
+      const bool row_ok = r < nrows;
+      const float rs = rv::keep_if(t[k].rs, row_ok);
+      float dot = 0.f;
+      float4 g[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const bool ok = row_ok && (FULL || lane_col<GL>(v, lane) < width);
+        t[k].x[v] = rv::keep_if(t[k].x[v], ok);
+        t[k].g[v] = rv::keep_if(t[k].g[v], ok);
+        g[v].x = t[k].g[v].x * wv[v].x;
+        g[v].y = t[k].g[v].y * wv[v].y;
+        g[v].z = t[k].g[v].z * wv[v].z;
+        g[v].w = t[k].g[v].w * wv[v].w;
+        g[v] = rv::keep_if(g[v], ok);
+        dot = dot + g[v].x * t[k].x[v].x;
+        dot = dot + g[v].y * t[k].x[v].y;
+        dot = dot + g[v].z * t[k].x[v].z;
+        dot = dot + g[v].w * t[k].x[v].w;
+      }
+      dot = rv::group_sum<GL>(dot);
+      const float c = ((dot / fwidth) * rs) * rs;
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        const float4 q = t[k].x[v];
+        // dweight partial: dy * (x * r), forward multiply order.
+        acc[v].x = acc[v].x + t[k].g[v].x * (q.x * rs);
+        acc[v].y = acc[v].y + t[k].g[v].y * (q.y * rs);
+        acc[v].z = acc[v].z + t[k].g[v].z * (q.z * rs);
+        acc[v].w = acc[v].w + t[k].g[v].w * (q.w * rs);
+        const int col = lane_col<GL>(v, lane);
+        if (row_ok && (FULL || col < width)) {
+          const unsigned off = (unsigned)(r * width + col);
+          float4 o;
+          o.x = (g[v].x - q.x * c) * rs;
+          o.y = (g[v].y - q.y * c) * rs;
+          o.z = (g[v].z - q.z * c) * rs;
+          o.w = (g[v].w - q.w * c) * rs;
+          if constexpr (ACC) {
+            o.x = o.x + t[k].h[v].x;
+            o.y = o.y + t[k].h[v].y;
+            o.z = o.z + t[k].h[v].z;
+            o.w = o.w + t[k].h[v].w;
+          }
+          if constexpr (H16) store_y(d16b + off, o);
+          if constexpr (PASS) {
+            o.x = o.x + t[k].p[v].x;
+            o.y = o.y + t[k].p[v].y;
+            o.z = o.z + t[k].p[v].z;
+            o.w = o.w + t[k].p[v].w;
+          }
+          rv::st_f4s(dxb + off, o);
+        }
+      }
+    }
+  }
+
+  // Column partials of the block's (wave, row-in-group) slots, summed in slot
+  // order: slot s = wave * 4 + sub holds float4 number v*16 + l%16 at [s][v*16 + l%16].
+  __shared__ float4 red[kGrpWaves * 4][VEC * GL];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) red[wave * 4 + sub][v * GL + (lane & (GL - 1))] = acc[v];
+  __syncthreads();
+  const int s = threadIdx.x;
+  if (s < VEC * GL) {
+    float4 q[kGrpWaves * 4];
+#pragma unroll
+    for (int k = 0; k < kGrpWaves * 4; ++k) q[k] = red[k][s];
+    float4 tsum = q[0];
+#pragma unroll
+    for (int k = 1; k < kGrpWaves * 4; ++k) {
+      tsum.x = tsum.x + q[k].x;
+      tsum.y = tsum.y + q[k].y;
+      tsum.z = tsum.z + q[k].z;
+      tsum.w = tsum.w + q[k].w;
+    }
+    const int col = s * 4;  // float4 number s of the row
+    if (col < width) rv::st_f4(partial + (int64_t)blockIdx.x * width + col, tsum);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Backward, any width <= 64 * EPL (scalar).  Same structure as the vector
 // kernel; element j of a lane is column j*64 + lane.
 // ---------------------------------------------------------------------------
@@ -511,12 +770,12 @@ void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
 
 // dw[col] = sum over parts of partial[part][col] (row-major, one contiguous
 // row per backward block).  A block covers 64 columns (lane = column) with
-// kRedWaves waves; wave k sums parts k, k + kRedWaves, ... in order (all of
-// its at most kRedPerWave loads are issued before the first add: one memory
-// round trip), then the waves' sums are added in wave order through LDS.
-// Fixed order throughout.
+// kRedWaves waves; wave k sums parts k, k + kRedWaves, ... in order, in
+// batches of kRedPerWave parts whose loads are all issued before the batch's
+// first add (one memory round trip per batch), then the waves' sums are
+// added in wave order through LDS.  Fixed order throughout.
 constexpr int kRedWaves = 16;
-constexpr int kRedPerWave = 16;  // parts per wave: nparts <= kRedWaves * kRedPerWave
+constexpr int kRedPerWave = 16;
 
 __global__ __launch_bounds__(kRedWaves * 64)
 void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
@@ -525,16 +784,18 @@ void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
   const int wave = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + lane;
   const int col_c = col < width ? col : width - 1;
-  float v[kRedPerWave];
-#pragma unroll
-  for (int i = 0; i < kRedPerWave; ++i) {
-    const int part = wave + i * kRedWaves;
-    v[i] = partial[(int64_t)(part < nparts ? part : nparts - 1) * width + col_c];
-  }
   float s = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += kRedWaves * kRedPerWave) {
+    float v[kRedPerWave];
 #pragma unroll
-  for (int i = 0; i < kRedPerWave; ++i)
-    if (wave + i * kRedWaves < nparts) s = s + v[i];
+    for (int i = 0; i < kRedPerWave; ++i) {
+      const int part = p0 + wave + i * kRedWaves;
+      v[i] = partial[(int64_t)(part < nparts ? part : nparts - 1) * width + col_c];
+    }
+#pragma unroll
+    for (int i = 0; i < kRedPerWave; ++i)
+      if (p0 + wave + i * kRedWaves < nparts) s = s + v[i];
+  }
   __shared__ float red[kRedWaves][64];
   red[wave][lane] = s;
   __syncthreads();
@@ -554,27 +815,67 @@ struct BwdPlan {
   int nparts;  // backward blocks = partial rows
 };
 
-// 256 blocks = one per compute unit on a 256-CU MI355X, all resident at
-// once, every block with the same number of rows (no partial second wave of
-// blocks).  The count is a constant, not a device query, so the dw summation
-// order -- and therefore dw bit for bit -- does not depend on the device.
-// (Reducing the partials inside this kernel instead -- the last block to
-// finish sums them -- needs device-scope release/acquire fences, which write
-// back the per-XCD L2 on MI355X and measured 4-15x slower than this second
-// launch.)
+// Wide rows (width > 256): 256 blocks = one per compute unit on a 256-CU
+// MI355X, all resident at once, every block with the same number of rows (no
+// partial second wave of blocks).  Rows of width <= 256 (rms_bwd_grp): blocks
+// of 64 .. 128 rows, at most 256 blocks up to 32768 rows.  The counts depend
+// on rows and width only, not on
+// the device, so the dw summation order -- and therefore dw bit for bit --
+// does not depend on the device.  (Reducing the partials inside the backward
+// kernel instead -- the last block to finish sums them -- needs device-scope
+// release/acquire fences, which write back the per-XCD L2 on MI355X and
+// measured 4-15x slower than this second launch.)
 constexpr int64_t kBwdTargetBlocks = RV_RMS_BWD_BLOCKS;
-static_assert(kBwdTargetBlocks <= kRedWaves * kRedPerWave,
-              "rms_dw_reduce sums at most kRedWaves * kRedPerWave partial rows");
 
-BwdPlan plan_bwd(int64_t rows) {
-  const int64_t target = kBwdTargetBlocks;
-  int64_t rpb = (rows + target - 1) / target;
+// Whether the backward of this width runs rms_bwd_grp (when the pointers allow
+// the vector path): the partial-row plan depends on it.
+constexpr bool bwd_narrow(int64_t width) { return width <= 256; }
+
+// Groups per wave of rms_bwd_grp for this many rows: 4, 5, 6 or 8 (the
+// instantiated counts).
+int grp_loads(int64_t rows) {
+  const int64_t per_wave = (rows + kBwdTargetBlocks * kGrpWaves * 4 - 1) /
+                           (kBwdTargetBlocks * kGrpWaves * 4);
+  if (per_wave <= kGrpMinLoads) return kGrpMinLoads;
+  if (per_wave <= 6) return (int)per_wave;
+  return kGrpMaxLoads;
+}
+
+BwdPlan plan_bwd(int64_t rows, int64_t width) {
+  int64_t rpb = bwd_narrow(width) ? (int64_t)kGrpWaves * 4 * grp_loads(rows)
+                                  : (rows + kBwdTargetBlocks - 1) / kBwdTargetBlocks;
   if (rpb < 1) rpb = 1;
   BwdPlan p;
   p.rows_per_block = rpb;
   p.nparts = (int)((rows + rpb - 1) / rpb);
   return p;
 }
+
+// Forward grid: with 16 lanes per row a wave per four-row group
+// (rms_fwd_grp); with 64 a persistent grid of RV_RMS_FWD_BLOCKS_PER_CU blocks
+// per CU (rms_fwd_vec).
+dim3 fwd_grid(int64_t rows, int lanes_per_row) {
+  const int64_t rows_per_block = (int64_t)kFwdWaves * (64 / lanes_per_row);
+  int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+  if (lanes_per_row == 64) {
+    const int64_t cap = (int64_t)rv_host::cu_count() * RV_RMS_FWD_BLOCKS_PER_CU;
+    if (blocks > cap) blocks = cap;
+  }
+  return dim3((unsigned)blocks);
+}
+
+// Vector layout by width: 16 lanes per row with 1, 2 or 4 float4 per lane up to
+// width 256; 64 lanes per row with 2 .. 16 float4 per lane above.
+#define RV_FWD_DISPATCH(W, LAUNCH)       \
+  do {                                   \
+    if ((W) <= 64) LAUNCH(1, 16);        \
+    else if ((W) <= 128) LAUNCH(2, 16);  \
+    else if ((W) <= 256) LAUNCH(4, 16);  \
+    else if ((W) <= 512) LAUNCH(2, 64);  \
+    else if ((W) <= 1024) LAUNCH(4, 64); \
+    else if ((W) <= 2048) LAUNCH(8, 64); \
+    else LAUNCH(16, 64);                 \
+  } while (0)
 
 template <typename F, bool ADD, typename Y = float>
 int launch_fwd(const float* x, const F* f, const float* w, float* h, Y* y,
@@ -587,22 +888,18 @@ int launch_fwd(const float* x, const F* f, const float* w, float* h, Y* y,
                    (f == nullptr ||
                     (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0);
   if (vec && width <= 256 * kMaxVec) {
-    constexpr int RPW = RV_RMS_FWD_RPW;
-    const int64_t rows_per_block = (int64_t)kFwdWaves * RPW;
-    int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
-    const int64_t cap = (int64_t)rv_host::cu_count() * RV_RMS_FWD_BLOCKS_PER_CU;
-    if (blocks > cap) blocks = cap;
-    const dim3 grid((unsigned)blocks);
-    const dim3 block(kFwdWaves * 64);
-    const int vecs = (width + 255) / 256;
-#define RV_FWD_VEC(V)                                                          \
-  hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, ADD, Y>), grid, block, 0, stream, x, f, \
-                     w, h, y, rstd, rows, width, eps)
-    if (vecs <= 1) RV_FWD_VEC(1);
-    else if (vecs <= 2) RV_FWD_VEC(2);
-    else if (vecs <= 4) RV_FWD_VEC(4);
-    else if (vecs <= 8) RV_FWD_VEC(8);
-    else RV_FWD_VEC(16);
+#define RV_FWD_VEC(V, G)                                                                      \
+  if constexpr (G == 16) {                                                                    \
+    if (width == 64 * (V))                                                                    \
+      hipLaunchKernelGGL((rms_fwd_grp<V, true, F, ADD, Y>), fwd_grid(rows, G),                \
+                         dim3(kFwdWaves * 64), 0, stream, x, f, w, h, y, rstd, rows, width, eps); \
+    else                                                                                      \
+      hipLaunchKernelGGL((rms_fwd_grp<V, false, F, ADD, Y>), fwd_grid(rows, G),               \
+                         dim3(kFwdWaves * 64), 0, stream, x, f, w, h, y, rstd, rows, width, eps); \
+  } else                                                                                      \
+    hipLaunchKernelGGL((rms_fwd_vec<V, G, F, ADD, Y>), fwd_grid(rows, G), dim3(kFwdWaves * 64), \
+                       0, stream, x, f, w, h, y, rstd, rows, width, eps)
+    RV_FWD_DISPATCH(width, RV_FWD_VEC);
 #undef RV_FWD_VEC
     return rv_host::check_launch();
   }
@@ -641,22 +938,21 @@ int launch_fwd_sub(const float* x, const F* f, const float* w, float* d, float* 
                    (reinterpret_cast<uintptr_t>(f) % (4 * sizeof(F))) == 0 &&
                    (reinterpret_cast<uintptr_t>(g) % (4 * sizeof(F))) == 0;
   if (!vec || width > 256 * kMaxVec) return RV_ERR_UNSUPPORTED;
-  constexpr int RPW = RV_RMS_FWD_RPW;
-  const int64_t rows_per_block = (int64_t)kFwdWaves * RPW;
-  int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
-  const int64_t cap = (int64_t)rv_host::cu_count() * RV_RMS_FWD_BLOCKS_PER_CU;
-  if (blocks > cap) blocks = cap;
-  const dim3 grid((unsigned)blocks);
-  const dim3 block(kFwdWaves * 64);
-  const int vecs = (width + 255) / 256;
-#define RV_FWD_SUB(V)                                                                      \
-  hipLaunchKernelGGL((rms_fwd_vec<V, RPW, F, true, __half, SUBM>), grid, block, 0, stream, x, \
-                     f, w, h, y, rstd, rows, width, eps, d, g, scale, sign)
-  if (vecs <= 1) RV_FWD_SUB(1);
-  else if (vecs <= 2) RV_FWD_SUB(2);
-  else if (vecs <= 4) RV_FWD_SUB(4);
-  else if (vecs <= 8) RV_FWD_SUB(8);
-  else RV_FWD_SUB(16);
+#define RV_FWD_SUB(V, G)                                                                       \
+  if constexpr (G == 16) {                                                                     \
+    if (width == 64 * (V))                                                                     \
+      hipLaunchKernelGGL((rms_fwd_grp<V, true, F, true, __half, SUBM>), fwd_grid(rows, G),     \
+                         dim3(kFwdWaves * 64), 0, stream, x, f, w, h, y, rstd, rows, width,    \
+                         eps, d, g, scale, sign);                                              \
+    else                                                                                       \
+      hipLaunchKernelGGL((rms_fwd_grp<V, false, F, true, __half, SUBM>), fwd_grid(rows, G),    \
+                         dim3(kFwdWaves * 64), 0, stream, x, f, w, h, y, rstd, rows, width,    \
+                         eps, d, g, scale, sign);                                              \
+  } else                                                                                       \
+    hipLaunchKernelGGL((rms_fwd_vec<V, G, F, true, __half, SUBM>), fwd_grid(rows, G),          \
+                       dim3(kFwdWaves * 64), 0, stream, x, f, w, h, y, rstd, rows, width, eps, \
+                       d, g, scale, sign)
+  RV_FWD_DISPATCH(width, RV_FWD_SUB);
 #undef RV_FWD_SUB
   return rv_host::check_launch();
 }
@@ -669,7 +965,7 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
   if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > 4096) return RV_ERR_UNSUPPORTED;
-  const BwdPlan p = plan_bwd(rows);
+  const BwdPlan p = plan_bwd(rows, width);
   const int64_t need = (int64_t)p.nparts * width * (int64_t)sizeof(float);
   if (workspace == nullptr || workspace_bytes < need) return RV_ERR_WORKSPACE;
   if (!rv_host::aligned16(workspace)) return RV_ERR_WORKSPACE;
@@ -686,7 +982,40 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
   if (!vec && (dh != nullptr || dx16 != nullptr || dpass != nullptr)) return RV_ERR_UNSUPPORTED;
   // the pass-through gradient: with the fp16 copy and without dh only
   if (dpass != nullptr && (dh != nullptr || dx16 == nullptr)) return RV_ERR_UNSUPPORTED;
-  if (vec) {
+  if (vec && bwd_narrow(iw)) {
+    const dim3 gblock(kGrpWaves * 64);
+    const int ng = grp_loads(rows);
+#define RV_BWD_GRP_K(V, NG, ACC, H16, PASS)                                                       \
+  do {                                                                                            \
+    if (iw == 64 * (V))                                                                           \
+      hipLaunchKernelGGL((rms_bwd_grp<V, NG, true, G, ACC, H16, PASS>), grid, gblock, 0, s, x, w, \
+                         dy, rstd, dx, partial, rows, iw, dh, dx16, dpass);                       \
+    else                                                                                          \
+      hipLaunchKernelGGL((rms_bwd_grp<V, NG, false, G, ACC, H16, PASS>), grid, gblock, 0, s, x,   \
+                         w, dy, rstd, dx, partial, rows, iw, dh, dx16, dpass);                    \
+  } while (0)
+#define RV_BWD_GRP_NG(V, NG)                                                      \
+  do {                                                                            \
+    if (dpass != nullptr) RV_BWD_GRP_K(V, NG, false, true, true);                 \
+    else if (dh != nullptr && dx16 != nullptr) RV_BWD_GRP_K(V, NG, true, true, false); \
+    else if (dh != nullptr) RV_BWD_GRP_K(V, NG, true, false, false);              \
+    else if (dx16 != nullptr) RV_BWD_GRP_K(V, NG, false, true, false);            \
+    else RV_BWD_GRP_K(V, NG, false, false, false);                                \
+  } while (0)
+#define RV_BWD_GRP(V)                          \
+  do {                                         \
+    if (ng <= 4) RV_BWD_GRP_NG(V, 4);          \
+    else if (ng == 5) RV_BWD_GRP_NG(V, 5);     \
+    else if (ng == 6) RV_BWD_GRP_NG(V, 6);     \
+    else RV_BWD_GRP_NG(V, 8);                  \
+  } while (0)
+    if (iw <= 64) RV_BWD_GRP(1);
+    else if (iw <= 128) RV_BWD_GRP(2);
+    else RV_BWD_GRP(4);
+#undef RV_BWD_GRP
+#undef RV_BWD_GRP_NG
+#undef RV_BWD_GRP_K
+  } else if (vec) {
     const int vecs = (iw + 255) / 256;
 #define RV_BWD_VEC_K(V, ACC, H16)                                                         \
   hipLaunchKernelGGL((rms_bwd_vec<V, bwd_waves(V, ACC), G, ACC, H16>), grid,              \
@@ -856,7 +1185,7 @@ int rv_midpoint_rmsnorm_fwd_f16(const float* p, const void* a, const void* m, in
 
 int64_t rv_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return -(int64_t)RV_ERR_BAD_SIZE;
-  const BwdPlan p = plan_bwd(rows);
+  const BwdPlan p = plan_bwd(rows, width);
   return (int64_t)p.nparts * width * (int64_t)sizeof(float);
 }
 
@@ -874,7 +1203,7 @@ int rv_rmsnorm_bwd_noalloc(const float* x, const float* w, const float* dy, cons
   if (!x || !w || !dy || !rstd || !dx || !dw) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || width <= 0) return RV_ERR_BAD_SIZE;
   if (width > kNoallocMaxWidth) return RV_ERR_UNSUPPORTED;
-  const int64_t need = (int64_t)plan_bwd(rows).nparts * width * (int64_t)sizeof(float);
+  const int64_t need = (int64_t)plan_bwd(rows, width).nparts * width * (int64_t)sizeof(float);
   if (need > kNoallocScratchFloats * (int64_t)sizeof(float)) return RV_ERR_WORKSPACE;
   float* ws = nullptr;
   const int st = scratch_address((hipStream_t)stream, &ws);

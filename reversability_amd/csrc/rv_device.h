@@ -39,6 +39,29 @@ __device__ __forceinline__ float wave_sum(float v) {
   return ((r0 + r1) + r2) + r3;
 }
 
+// Sum over each 16-lane DPP row, the same bits in all 16 lanes: xor-1 and
+// xor-2 (quad_perm) leave every lane of a quad with the same quad sum, then
+// row_half_mirror (lane i with 7 - i of its 8-lane half) and row_mirror (i
+// with 15 - i) add partners that hold the same-order partial sums, so each
+// add is a + b in one lane and b + a in its partner: bitwise equal.  The
+// result is ((q0 + q1) + (q2 + q3)) of the four quad sums q.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp_mov<0x141>(v);  // row_half_mirror
+  v = v + dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
+// Sum over a group of G lanes (a row of the RMSNorm layouts), the same value
+// in every lane of the group: G = 16 (one DPP row) or 64 (the wave).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(G == 16 || G == 64, "lane groups of 16 or 64");
+  if constexpr (G == 16) return row16_sum(v);
+  else return wave_sum(v);
+}
+
 // ---------------------------------------------------------------------------
 // dtype plumbing
 // ---------------------------------------------------------------------------

@@ -64,10 +64,19 @@ def test_argument_validation_without_device():
     assert lib.rv_add_rmsnorm_fwd(fake, fake, _hip.RV_F64, fake, fake, fake, fake, 4, 256, 1e-7, None) == 3
 
 
-@pytest.mark.parametrize("rows,width", [(1, 8), (14848, 256), (32768, 1024), (69, 33)])
+@pytest.mark.parametrize("rows,width", [(1, 8), (14848, 256), (32768, 1024), (69, 33),
+                                        (16896, 256), (24000, 256), (27000, 256),
+                                        (40000, 256), (300, 260)])
 def test_workspace_size_is_device_independent(rows, width):
+    """Partial rows: width <= 256 -- one per 16 g rows, g = ceil(rows / 4096)
+    groups per wave clamped to 4 .. 8 (7 taken as 8); wider -- 256 blocks of
+    ceil(rows / 256) rows."""
     n = _hip.rmsnorm_workspace_bytes(rows, width)
-    per_block = -(-rows // 256)
+    if width <= 256:
+        g = min(max(-(-rows // 4096), 4), 8)
+        per_block = 16 * (8 if g == 7 else g)
+    else:
+        per_block = -(-rows // 256)
     parts = -(-rows // per_block)
     assert n == parts * width * 4
 

@@ -74,6 +74,12 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(cuda_device):
     st = lib.rv_rmsnorm_bwd_noalloc(x.data_ptr(), w.data_ptr(), x.data_ptr(), rstd.data_ptr(),
                                     x.data_ptr(), w.data_ptr(), 4, 8192, _hip._stream(x))
     assert st == 3  # RV_ERR_UNSUPPORTED: width above the 4096 the scratch is sized for
+    # width <= 256: one partial row per 128 rows at this size; 524289 rows need
+    # 4097 rows of 256 floats, one more than the 4 MiB scratch holds (rejected
+    # before any launch)
+    st = lib.rv_rmsnorm_bwd_noalloc(x.data_ptr(), w.data_ptr(), x.data_ptr(), rstd.data_ptr(),
+                                    x.data_ptr(), w.data_ptr(), 524289, 256, _hip._stream(x))
+    assert st == 4  # RV_ERR_WORKSPACE
     assert lib.rv_rmsnorm_bwd_noalloc(None, w.data_ptr(), x.data_ptr(), rstd.data_ptr(),
                                       x.data_ptr(), w.data_ptr(), 4, 256, None) == 1
     assert lib.rv_rmsnorm_bwd_noalloc(ctypes.c_void_p(x.data_ptr()), w.data_ptr(), x.data_ptr(),
