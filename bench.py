@@ -3,8 +3,10 @@
 Headline (``value``): fused RMSNorm + SwiGLU forward+backward throughput in
 algorithmic HBM GB/s.  One step = RMSNorm fwd + bwd over configs[0]
 (x fp32 [14848, 256]) followed by SwiGLU fwd + bwd over configs[1]
-(gate/up fp16 [14848, 1024]), launched through the C ABI on torch's current
-stream.  Algorithmic bytes per step (each tensor read or written once):
+(gate/up fp16 [14848, 1024]), launched through the C ABI; the timed steps
+are captured in one HIP graph and replayed (the eagerly launched step is
+reported beside it).  Algorithmic bytes per step (each tensor read or written
+once):
 
     RMSNorm fwd  x r, w r, y w, rstd w             30,469,120 B
     RMSNorm bwd  x r, dy r, rstd r, w r, dx w, dw w 45,674,496 B
@@ -19,8 +21,8 @@ launch reads data last touched a full rotation earlier.
 
 Also reported, on the same line:
   roofline      the dominant kernel (SwiGLU backward): its algorithmic bytes
-                divided by its average duration (HIP events around a run of
-                back-to-back launches of that kernel on its launch stream),
+                divided by its average duration (HIP events around replays
+                of a HIP graph of back-to-back launches of that kernel),
                 against the 8 TB/s HBM peak; ``traffic`` is the HBM bytes per
                 launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs
                 (profiles/traffic.json), if recorded.
@@ -158,8 +160,11 @@ class KernelStep:
         sets = self.rms_sets if name.startswith("rms") else self.sw_sets
         return sets[i % len(sets)]
 
-    def run_one(self, name: str, i: int) -> None:
-        rc = self.fns[name](*self.set_for(name, i)["args"][name], self.stream)
+    def run_one(self, name: str, i: int, stream=None) -> None:
+        """One launch of ``name`` on set i, on ``stream`` (a hipStream_t value;
+        default: the stream torch had at construction)."""
+        rc = self.fns[name](*self.set_for(name, i)["args"][name],
+                            self.stream if stream is None else stream)
         if rc:
             raise RuntimeError(f"{name} failed with status {rc}")
 
@@ -168,14 +173,44 @@ class KernelStep:
             self.run_one(name, i)
 
 
+def graph_time_ms(launch, count: int, replays: int = 3) -> float:
+    """Average device time (ms) of one launch: ``count`` calls of
+    ``launch(i, stream)`` captured back to back in one HIP graph, replayed
+    ``replays`` times between two HIP events on the replay stream.  Kernels a
+    few microseconds long launched one by one from Python are bound by the
+    host's launch rate (ctypes call + hipLaunchKernel, ~7-8 us per call on the
+    MI355X boxes); a replayed graph issues them back to back, so the average
+    is the kernels' own duration, the quantity rocprofv3 --kernel-trace
+    reports."""
+    import torch
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stream = torch.cuda.current_stream().cuda_stream
+        for i in range(count):
+            launch(i, stream)
+    graph.replay()  # warm-up replay (clocks, caches, code objects)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / (replays * count)
+    del graph
+    return ms
+
+
 def time_kernels(dev, steps: int, warmup: int):
     """Headline step timing plus per-kernel averages.
 
-    Per-kernel: the kernel alone, ``steps`` launches back to back over the
-    rotating buffer sets, one HIP event pair around them on the launch stream
-    (average = elapsed / launches).  Consecutive same-stream kernels on the
-    MI355X start when the previous one ends, so this average is the kernel's
-    own duration, the quantity rocprofv3 --kernel-trace reports.
+    Step: ``steps`` steps (each the four ops over its rotating buffer sets)
+    captured in one HIP graph and replayed, wall clock of the replays between
+    two synchronizations -- the way the training steps below are launched --
+    and, beside it, the same steps launched one by one from Python on torch's
+    current stream (``eager``).  Per kernel: the kernel alone, ``steps``
+    launches over the rotating buffer sets captured in a HIP graph and
+    replayed (``graph_time_ms``).
     """
     import torch
     step = KernelStep(dev)
@@ -186,18 +221,26 @@ def time_kernels(dev, steps: int, warmup: int):
     for i in range(steps):
         step.run(i)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    eager = (time.perf_counter() - t0) / steps
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stream = torch.cuda.current_stream().cuda_stream
+        for i in range(steps):
+            for name in step.order:
+                step.run_one(name, i, stream)
+    graph.replay()  # untimed replay: the warm-up of the captured steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    graph.replay()  # exactly ``steps`` timed steps
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    del graph
     per_kernel = {}
     for name in step.order:
-        for i in range(max(warmup, 100)):  # let clocks settle on the short kernels
+        for i in range(max(warmup, 20)):
             step.run_one(name, i)
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for i in range(steps):
-            step.run_one(name, i)
-        stop.record()
-        torch.cuda.synchronize()
-        per_kernel[name] = start.elapsed_time(stop) / steps  # ms
+        per_kernel[name] = graph_time_ms(
+            lambda i, stream, name=name: step.run_one(name, i, stream), steps)
     ceiling = copy_ceilings(dev, steps)
     # determinism spot check: relaunch the last sets, compare outputs bitwise
     r, w = step.set_for("rms_bwd", steps - 1), step.set_for("sw_bwd", steps - 1)
@@ -209,16 +252,16 @@ def time_kernels(dev, steps: int, warmup: int):
     if not (torch.equal(ref_dx, r["dx"]) and torch.equal(ref_du, w["du"])
             and torch.equal(ref_dw, r["dw"])):
         raise RuntimeError("kernel outputs are not run-to-run deterministic")
-    return wall / steps, per_kernel, ceiling
+    return wall, eager, per_kernel, ceiling
 
 
 def copy_ceilings(dev, launches: int) -> dict:
     """Average duration (ms) of torch's own elementwise kernels moving each
     kernel's bytes, on rotating buffers (> 1.5 GB per shape), timed like the
-    kernels: RMSNorm fwd = mul [14848, 256] fp32 (1 read, 1 write); RMSNorm
-    bwd = add [14848, 256] fp32 (2 reads, 1 write); SwiGLU fwd = add
-    [14848, 1024] fp16 (2 reads, 1 write); SwiGLU bwd = mul [14848, 2560] fp16
-    (1 read, 1 write of 76 MB each: its 152 MB total)."""
+    kernels (``graph_time_ms``): RMSNorm fwd = mul [14848, 256] fp32 (1 read,
+    1 write); RMSNorm bwd = add [14848, 256] fp32 (2 reads, 1 write); SwiGLU
+    fwd = add [14848, 1024] fp16 (2 reads, 1 write); SwiGLU bwd = mul
+    [14848, 2560] fp16 (1 read, 1 write of 76 MB each: its 152 MB total)."""
     import torch
     shapes = {"rms_fwd": ((ROWS, D_MODEL), torch.float32, 1),
               "rms_bwd": ((ROWS, D_MODEL), torch.float32, 2),
@@ -231,21 +274,15 @@ def copy_ceilings(dev, launches: int) -> dict:
         sets = [[torch.ones(shape, device=dev, dtype=dtype) for _ in range(reads + 1)]
                 for _ in range(nsets)]
 
-        def run(i, sets=sets, reads=reads):
+        def run(i, stream=None, sets=sets, reads=reads):
             t = sets[i % len(sets)]
             if reads == 1:
                 torch.mul(t[0], 2.0, out=t[1])
             else:
                 torch.add(t[0], t[1], out=t[2])
-        for i in range(max(20, 100)):
+        for i in range(20):
             run(i)
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for i in range(launches):
-            run(i)
-        stop.record()
-        torch.cuda.synchronize()
-        out[name] = start.elapsed_time(stop) / launches
+        out[name] = graph_time_ms(run, launches)
         del sets
     torch.cuda.empty_cache()
     return out
@@ -732,7 +769,7 @@ def main() -> int:
         print(json.dumps({"attention": attention_bench(dev), "embedding": embedding_bench(dev)}),
               flush=True)
         return 0
-    ms_step_s, per_kernel, ceiling = time_kernels(dev, args.steps, args.warmup)
+    ms_step_s, eager_s, per_kernel, ceiling = time_kernels(dev, args.steps, args.warmup)
     value = STEP_BYTES / ms_step_s / 1e9
     bytes_by = {"rms_fwd": RMS_FWD_BYTES, "rms_bwd": RMS_BWD_BYTES,
                 "sw_fwd": SW_FWD_BYTES, "sw_bwd": SW_BWD_BYTES}
@@ -763,6 +800,10 @@ def main() -> int:
                    "buffer_sets": {"rmsnorm": RMS_SETS, "swiglu": SW_SETS},
                    "step_bytes": STEP_BYTES},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "launch": "HIP graph of the timed steps, replayed",
+        "eager": {"GBps": round(STEP_BYTES / eager_s / 1e9, 2), "ms_per_step": eager_s * 1e3,
+                  "what": "the same steps launched one by one from Python (ctypes) on "
+                          "torch's current stream"},
         "copy_ceiling": {"GBps": round(ceiling_gbs, 1),
                          "frac_of_peak": round(ceiling_gbs / HBM_PEAK_GBS, 4),
                          "value_over_ceiling": round(value / ceiling_gbs, 4),

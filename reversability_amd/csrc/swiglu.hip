@@ -40,142 +40,71 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
 
 constexpr int kThreads = 256;
 
-// Launch shapes and cache hints chosen by timing sweeps on MI355X at
-// [14848, 1024] fp16 over > 1.5 GB of rotating buffers: one 16-byte vector
-// per operand per thread per iteration; forward 4 blocks per CU with
-// streaming loads, backward 2 blocks per CU with streaming loads and stores.
-#ifndef RV_SWIGLU_VPT
-#define RV_SWIGLU_VPT 1
-#endif
-#ifndef RV_SWIGLU_FWD_BLOCKS_PER_CU
-#define RV_SWIGLU_FWD_BLOCKS_PER_CU 4
-#endif
-#ifndef RV_SWIGLU_BWD_BLOCKS_PER_CU
-#define RV_SWIGLU_BWD_BLOCKS_PER_CU 2
-#endif
-constexpr int kVpt = RV_SWIGLU_VPT;
+// Cache hints chosen by timing sweeps on MI355X at [14848, 1024] fp16 over
+// > 1.5 GB of rotating buffers: streaming (nt) loads in both directions,
+// streaming stores in the backward, plain stores in the forward.
 constexpr bool kFwdNtStore = false;
 constexpr bool kBwdNtStore = true;
 
-// Persistent, software-pipelined streaming: each block walks the vector index
-// space with a grid-sized stride, alternating between two register tiles.
-// The loads of the next tile are issued before the math of the current one,
-// so the sigmoid's transcendental work (two quarter-rate ops per element)
-// overlaps HBM latency instead of alternating with it.  Prefetches are
-// unconditional: an index past the end is clamped to the last vector, so
-// those loads all hit one cached line, and no branch forces the compiler to
-// drain the load queue (s_waitcnt vmcnt(0)) inside the loop.
-template <typename T>
-struct SwiGLUTile {
+// A grid with one thread per U 16-byte vectors of every operand (vector
+// index blockIdx.x * 256 U + k * 256 + threadIdx.x, k < U), no loop; every
+// load of a thread is issued before its first wait, and the sigmoid's
+// transcendental work of one wave overlaps the loads of the others.  C2
+// (same rotating-buffer timing as above): forward with U = 2 15.8 us and
+// backward with U = 1 25.2 us, against 16.5 and 25.8 for a persistent
+// grid-stride loop with the next vector's loads issued before the current
+// one's math.
+template <typename T, bool BWD, int U>
+__global__ __launch_bounds__(kThreads)
+void swiglu_once(const T* __restrict__ u, int64_t ld_u, const T* __restrict__ dy,
+                 T* __restrict__ out, int64_t width, FastDiv vpr, uint32_t total) {
   using V = rv::Vec16<T>;
-  V g[kVpt], v[kVpt], d[kVpt];
-};
-
-template <typename T, bool BWD>
-__device__ __forceinline__ void swiglu_load(SwiGLUTile<T>& t, const T* __restrict__ u,
-                                            int64_t ld_u, const T* __restrict__ dy,
-                                            int64_t width, const FastDiv& vpr,
-                                            uint32_t first, uint32_t total) {
-  constexpr int N = rv::Vec16<T>::N;
+  constexpr int N = V::N;
+  const uint32_t first = blockIdx.x * (uint32_t)(kThreads * U) + threadIdx.x;
+  V g[U], v[U], d[BWD ? U : 1];
 #pragma unroll
-  for (int k = 0; k < kVpt; ++k) {
+  for (int k = 0; k < U; ++k) {
     uint32_t i = first + k * kThreads;
     i = i < total ? i : total - 1;  // clamp: always a valid address
     const uint32_t row = fdiv(i, vpr);
     const int64_t c = (int64_t)(i - row * vpr.d) * N;
     const T* src = u + (int64_t)row * ld_u + c;
-    t.g[k] = rv::load16<true>(src);
-    t.v[k] = rv::load16<true>(src + width);
-    if constexpr (BWD) t.d[k] = rv::load16<true>(dy + (int64_t)row * width + c);
+    g[k] = rv::load16<true>(src);
+    v[k] = rv::load16<true>(src + width);
+    if constexpr (BWD) d[k] = rv::load16<true>(dy + (int64_t)row * width + c);
   }
-}
-
-template <typename T>
-__device__ __forceinline__ void swiglu_fwd_compute(const SwiGLUTile<T>& t, T* __restrict__ o,
-                                                   int64_t width, const FastDiv& vpr,
-                                                   uint32_t first, uint32_t total) {
-  using V = rv::Vec16<T>;
-  constexpr int N = V::N;
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int k = 0; k < kVpt; ++k) {
+  for (int k = 0; k < U; ++k) {
     const uint32_t i = first + k * kThreads;
-    V out;
+    V a, b;
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      const float gf = rv::Conv<T>::to_f(t.g[k].v[e]);
-      const float silu = rv::round_to<T>(gf * rv::fast_sigmoid(gf));
-      out.v[e] = rv::Conv<T>::from_f(silu * rv::Conv<T>::to_f(t.v[k].v[e]));
+      const float gf = rv::Conv<T>::to_f(g[k].v[e]);
+      const float vf = rv::Conv<T>::to_f(v[k].v[e]);
+      if constexpr (BWD) {
+        const float df = rv::Conv<T>::to_f(d[k].v[e]);
+        const float sg = rv::fast_sigmoid(gf);
+        const float silu = rv::round_to<T>(gf * sg);
+        const float dgi = rv::round_to<T>(df * vf);
+        a.v[e] = rv::Conv<T>::from_f(dgi * (sg * (1.0f + gf * (1.0f - sg))));
+        b.v[e] = rv::Conv<T>::from_f(df * silu);
+      } else {
+        const float silu = rv::round_to<T>(gf * rv::fast_sigmoid(gf));
+        a.v[e] = rv::Conv<T>::from_f(silu * vf);
+      }
     }
     if (i < total) {
       const uint32_t row = fdiv(i, vpr);
       const int64_t c = (int64_t)(i - row * vpr.d) * N;
-      rv::store16<kFwdNtStore>(o + (int64_t)row * width + c, out);
+      if constexpr (BWD) {
+        T* dst = out + (int64_t)row * ld_u + c;
+        rv::store16<kBwdNtStore>(dst, a);
+        rv::store16<kBwdNtStore>(dst + width, b);
+      } else {
+        rv::store16<kFwdNtStore>(out + (int64_t)row * width + c, a);
+      }
     }
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void swiglu_bwd_compute(const SwiGLUTile<T>& t, T* __restrict__ du,
-                                                   int64_t ld_u, int64_t width,
-                                                   const FastDiv& vpr, uint32_t first,
-                                                   uint32_t total) {
-  using V = rv::Vec16<T>;
-  constexpr int N = V::N;
-#pragma unroll
-  for (int k = 0; k < kVpt; ++k) {
-    const uint32_t i = first + k * kThreads;
-    V dg, dv;
-#pragma unroll
-    for (int e = 0; e < N; ++e) {
-      const float gf = rv::Conv<T>::to_f(t.g[k].v[e]);
-      const float vf = rv::Conv<T>::to_f(t.v[k].v[e]);
-      const float df = rv::Conv<T>::to_f(t.d[k].v[e]);
-      const float s = rv::fast_sigmoid(gf);
-      const float silu = rv::round_to<T>(gf * s);
-      const float dgi = rv::round_to<T>(df * vf);
-      dg.v[e] = rv::Conv<T>::from_f(dgi * (s * (1.0f + gf * (1.0f - s))));
-      dv.v[e] = rv::Conv<T>::from_f(df * silu);
-    }
-    if (i < total) {
-      const uint32_t row = fdiv(i, vpr);
-      const int64_t c = (int64_t)(i - row * vpr.d) * N;
-      T* dst = du + (int64_t)row * ld_u + c;
-      rv::store16<kBwdNtStore>(dst, dg);
-      rv::store16<kBwdNtStore>(dst + width, dv);
-    }
-  }
-}
-
-template <typename T, bool BWD>
-__device__ __forceinline__ void swiglu_compute(const SwiGLUTile<T>& t, T* __restrict__ out,
-                                               int64_t ld_u, int64_t width, const FastDiv& vpr,
-                                               uint32_t first, uint32_t total) {
-  if constexpr (BWD)
-    swiglu_bwd_compute<T>(t, out, ld_u, width, vpr, first, total);
-  else
-    swiglu_fwd_compute<T>(t, out, width, vpr, first, total);
-}
-
-template <typename T, bool BWD>
-__global__ __launch_bounds__(kThreads)
-void swiglu_stream(const T* __restrict__ u, int64_t ld_u, const T* __restrict__ dy,
-                   T* __restrict__ out, int64_t width, FastDiv vpr, uint32_t total) {
-  const uint32_t step = gridDim.x * (uint32_t)(kThreads * kVpt);
-  const uint32_t block_first = blockIdx.x * (uint32_t)(kThreads * kVpt);
-  if (block_first >= total) return;  // block-uniform
-  // iterations of this block: block_first + k*step < total
-  const uint32_t iters = (total - 1 - block_first) / step + 1;
-  uint32_t first = block_first + threadIdx.x;
-  SwiGLUTile<T> a, b;
-  swiglu_load<T, BWD>(a, u, ld_u, dy, width, vpr, first, total);
-  for (uint32_t k = 0; k < iters; k += 2) {
-    swiglu_load<T, BWD>(b, u, ld_u, dy, width, vpr, first + step, total);
-    swiglu_compute<T, BWD>(a, out, ld_u, width, vpr, first, total);
-    if (k + 1 >= iters) break;
-    first += step;
-    swiglu_load<T, BWD>(a, u, ld_u, dy, width, vpr, first + step, total);
-    swiglu_compute<T, BWD>(b, out, ld_u, width, vpr, first, total);
-    first += step;
   }
 }
 
@@ -231,11 +160,11 @@ unsigned scalar_grid(int64_t n) {
   return (unsigned)(blocks < cap ? blocks : cap);
 }
 
-unsigned stream_grid(uint32_t total, int blocks_per_cu) {
-  const int64_t tiles = ((int64_t)total + kThreads * kVpt - 1) / (kThreads * kVpt);
-  const int64_t cap = (int64_t)rv_host::cu_count() * blocks_per_cu;
-  return (unsigned)(tiles < cap ? tiles : cap);
+unsigned once_grid(uint32_t total, int vectors_per_thread) {
+  const int64_t per_block = (int64_t)kThreads * vectors_per_thread;
+  return (unsigned)(((int64_t)total + per_block - 1) / per_block);
 }
+
 
 template <typename T>
 int launch_fwd(const T* u, int64_t ld_u, T* o, int64_t rows, int64_t width,
@@ -244,9 +173,9 @@ int launch_fwd(const T* u, int64_t ld_u, T* o, int64_t rows, int64_t width,
     constexpr int N = 16 / sizeof(T);
     const uint32_t total = (uint32_t)(rows * (width / N));
     const FastDiv vpr = make_fastdiv((uint32_t)(width / N));
-    hipLaunchKernelGGL((swiglu_stream<T, false>),
-                       dim3(stream_grid(total, RV_SWIGLU_FWD_BLOCKS_PER_CU)), dim3(kThreads),
-                       0, s, u, ld_u, (const T*)nullptr, o, width, vpr, total);
+    constexpr int U = 2;
+    hipLaunchKernelGGL((swiglu_once<T, false, U>), dim3(once_grid(total, U)), dim3(kThreads), 0,
+                       s, u, ld_u, (const T*)nullptr, o, width, vpr, total);
   } else {
     hipLaunchKernelGGL((swiglu_fwd_scalar<T>), dim3(scalar_grid(rows * width)),
                        dim3(kThreads), 0, s, u, ld_u, o, rows, width);
@@ -261,9 +190,9 @@ int launch_bwd(const T* u, int64_t ld_u, const T* dy, T* du, int64_t rows,
     constexpr int N = 16 / sizeof(T);
     const uint32_t total = (uint32_t)(rows * (width / N));
     const FastDiv vpr = make_fastdiv((uint32_t)(width / N));
-    hipLaunchKernelGGL((swiglu_stream<T, true>),
-                       dim3(stream_grid(total, RV_SWIGLU_BWD_BLOCKS_PER_CU)), dim3(kThreads),
-                       0, s, u, ld_u, dy, du, width, vpr, total);
+    constexpr int U = 1;
+    hipLaunchKernelGGL((swiglu_once<T, true, U>), dim3(once_grid(total, U)), dim3(kThreads), 0,
+                       s, u, ld_u, dy, du, width, vpr, total);
   } else {
     hipLaunchKernelGGL((swiglu_bwd_scalar<T>), dim3(scalar_grid(rows * width)),
                        dim3(kThreads), 0, s, u, ld_u, dy, du, rows, width);
