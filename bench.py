@@ -810,7 +810,7 @@ def main() -> int:
                          "what": "the step's bytes moved by torch's elementwise mul/add "
                                  "kernels of the same read/write shape, summed over the "
                                  "four kernels (copy_ceiling_us per kernel)"},
-        "roofline": {"bound": "hbm", "kernel": "swiglu_bwd_vec<fp16>",
+        "roofline": {"bound": "hbm", "kernel": "swiglu_once<__half, true, 1> (SwiGLU bwd)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "algorithmic_bytes": SW_BWD_BYTES},
