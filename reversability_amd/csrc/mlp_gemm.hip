@@ -496,7 +496,7 @@ void gemm_kernel(GemmArgs args) {
           __builtin_nontemporal_store(vw, reinterpret_cast<u32x4*>(u + row * args.ldu + args.f + col));
         }
       }
-    } else {
+    } else if constexpr (EPI == Epi::StoreF16) {
       constexpr int CPR = WN / 8, RPP = 64 / CPR;
       const int c = lane % CPR;
       const int64_t col = n0 + wn * WN + c * 8;
@@ -505,30 +505,56 @@ void gemm_kernel(GemmArgs args) {
         const int64_t row = row0 + r;
         if (row >= args.m) break;
         const u32x4 dw = *reinterpret_cast<const u32x4*>(stage + r * S + c * 8);
-        if constexpr (EPI == Epi::StoreF16) {
-          __builtin_nontemporal_store(dw, reinterpret_cast<u32x4*>(static_cast<__half*>(args.c) + row * args.ldc + col));
-        } else {  // SwiGLUBwd: du from u = [gate | value] and d_o = fp16(acc)
-          const __half* ur = static_cast<const __half*>(args.u) + row * args.ldu;
-          const u32x4 gw = *reinterpret_cast<const u32x4*>(ur + col);
-          const u32x4 vw = *reinterpret_cast<const u32x4*>(ur + args.f + col);
-          const __half* dh = reinterpret_cast<const __half*>(&dw);
-          const __half* gh = reinterpret_cast<const __half*>(&gw);
-          const __half* vh = reinterpret_cast<const __half*>(&vw);
-          __half dgo[8], dvo[8];
+        __builtin_nontemporal_store(dw, reinterpret_cast<u32x4*>(static_cast<__half*>(args.c) + row * args.ldc + col));
+      }
+    } else {
+      // SwiGLUBwd: du from u = [gate | value] and d_o = fp16(acc).  The u
+      // reads of up to 16 of a lane's rows are issued together (the
+      // accumulators are in LDS by now, their registers free), so the tile's
+      // epilogue waits on one memory round trip per 16 rows instead of one
+      // per 4; rows past m read the last row and store nothing.
+      constexpr int CPR = WN / 8, RPP = 64 / CPR;
+      constexpr int ITER = WM / RPP;              // rows per lane
+      constexpr int CH = ITER < 16 ? ITER : 16;   // rows whose u reads are in flight together
+      static_assert(ITER % CH == 0, "epilogue row chunks");
+      const int c = lane % CPR;
+      const int64_t col = n0 + wn * WN + c * 8;
+      const __half* ubase = static_cast<const __half*>(args.u);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float d = __half2float(dh[e]);
-            const float g = __half2float(gh[e]);
-            const float v = __half2float(vh[e]);
-            const float sg = rv::fast_sigmoid(g);
-            const float silu = rv::round_to<__half>(g * sg);
-            const float dgi = rv::round_to<__half>(d * v);
-            dgo[e] = __float2half_rn(dgi * (sg * (1.0f + g * (1.0f - sg))));
-            dvo[e] = __float2half_rn(d * silu);
+      for (int r0 = 0; r0 < ITER; r0 += CH) {
+        u32x4 gw[CH], vw[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          const int64_t rr = row0 + lane / CPR + (r0 + i) * RPP;
+          const __half* ur = ubase + (rr < args.m ? rr : args.m - 1) * args.ldu;
+          gw[i] = *reinterpret_cast<const u32x4*>(ur + col);
+          vw[i] = *reinterpret_cast<const u32x4*>(ur + args.f + col);
+        }
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+          const int r = lane / CPR + (r0 + i) * RPP;
+          const int64_t row = row0 + r;
+          if (row < args.m) {
+            const u32x4 dw = *reinterpret_cast<const u32x4*>(stage + r * S + c * 8);
+            const __half* dh = reinterpret_cast<const __half*>(&dw);
+            const __half* gh = reinterpret_cast<const __half*>(&gw[i]);
+            const __half* vh = reinterpret_cast<const __half*>(&vw[i]);
+            __half dgo[8], dvo[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float d = __half2float(dh[e]);
+              const float g = __half2float(gh[e]);
+              const float v = __half2float(vh[e]);
+              const float sg = rv::fast_sigmoid(g);
+              const float silu = rv::round_to<__half>(g * sg);
+              const float dgi = rv::round_to<__half>(d * v);
+              dgo[e] = __float2half_rn(dgi * (sg * (1.0f + g * (1.0f - sg))));
+              dvo[e] = __float2half_rn(d * silu);
+            }
+            __half* du = static_cast<__half*>(args.c) + row * args.ldc;
+            __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(dgo), reinterpret_cast<u32x4*>(du + col));
+            __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(dvo), reinterpret_cast<u32x4*>(du + args.f + col));
           }
-          __half* du = static_cast<__half*>(args.c) + row * args.ldc;
-          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(dgo), reinterpret_cast<u32x4*>(du + col));
-          __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(dvo), reinterpret_cast<u32x4*>(du + args.f + col));
         }
       }
     }
