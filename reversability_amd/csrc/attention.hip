@@ -102,23 +102,36 @@ __device__ __forceinline__ f16x8 pack8(const f32x16& v, int h) {
   return r;
 }
 
-// Global -> registers -> LDS copy of a tile of kTile rows x HD halves; rows at
-// or past `valid` are zero.
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer resource, gfx9 data format
+
+// Global -> registers -> LDS copy of a tile of kTile rows x HD halves.  The
+// loads go through a buffer resource that starts at the tile's first row and
+// ends with row `valid - 1`'s HD halves: rows at or past `valid` read as zero
+// (the buffer range check), so no row needs a predicate, and a thread's byte
+// offset inside a tile is the same for every tile (row stride `stride`
+// halves; launch checks keep kTile rows of it below 2 GiB).
 template <int HD>
 struct TileCopy {
   static constexpr int kPer = kTile * HD / 8 / kThreads;
   static_assert(kPer >= 1, "tile smaller than one chunk per thread");
   u32x4 v[kPer];
-  __device__ __forceinline__ void load(const __half* base, int64_t stride, int row0, int valid) {
+  uint32_t off[kPer];
+  __device__ __forceinline__ explicit TileCopy(int64_t stride) {
 #pragma unroll
     for (int it = 0; it < kPer; ++it) {
       const int ch = it * kThreads + threadIdx.x;
       const int r = ch / (HD / 8), c = ch % (HD / 8);
-      if (row0 + r < valid)
-        v[it] = *reinterpret_cast<const u32x4*>(base + (int64_t)(row0 + r) * stride + c * 8);
-      else
-        v[it] = u32x4{0u, 0u, 0u, 0u};
+      off[it] = (uint32_t)(((int64_t)r * stride + c * 8) * 2);
     }
+  }
+  __device__ __forceinline__ void load(const __half* base, int64_t stride, int row0, int valid) {
+    const int rows = min(valid - row0, kTile);
+    const int bytes = rows > 0 ? (int)(((int64_t)(rows - 1) * stride + HD) * 2) : 0;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<__half*>(base + (int64_t)row0 * stride), 0, bytes, kRsrcWord3);
+#pragma unroll
+    for (int it = 0; it < kPer; ++it)
+      v[it] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off[it], 0, 0);
   }
   __device__ __forceinline__ void store(_Float16* t) const {
 #pragma unroll
@@ -306,7 +319,7 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
 
   const int kv_end = min(T, qt * kBlockRows + kBlockRows);
   const int n_kt = (kv_end + kTile - 1) / kTile;
-  TileCopy<HD> ck, cv;
+  TileCopy<HD> ck(rs), cv(rs);
   ck.load(kb, rs, 0, T);
   cv.load(vb, rs, 0, T);
   ck.store(lds[0][0]);
@@ -509,7 +522,7 @@ void attn_bwd_kv_k(const __half* __restrict__ qkv, const __half* __restrict__ do
   }
 
   const int n_qtiles = (T - kbase + kTile - 1) / kTile;
-  TileCopy<HD> cq, cg;
+  TileCopy<HD> cq(rs), cg(os);
   cq.load(qb, rs, kbase, T);
   cg.load(gb, os, kbase, T);
   float lv = load_rowval(lb, kbase, T), dvv = load_rowval(db, kbase, T);
@@ -610,7 +623,7 @@ void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ dou
 
   const int kv_end = min(T, qt * kBlockRows + kBlockRows);
   const int n_kt = (kv_end + kTile - 1) / kTile;
-  TileCopy<HD> ck, cv;
+  TileCopy<HD> ck(rs), cv(rs);
   ck.load(kb, rs, 0, T);
   cv.load(vb, rs, 0, T);
   ck.store(lds[0][0]);
@@ -659,9 +672,12 @@ void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ dou
   }
 }
 
+// Sizes the kernels take: a kTile-row tile of qkv (row stride 3 H hd halves)
+// spans less than 2 GiB, so a tile's buffer resource and byte offsets fit.
 bool dims_ok(int64_t batch, int64_t seq, int64_t heads, int64_t hd) {
   return batch > 0 && seq > 0 && heads > 0 && (hd == 32 || hd == 64 || hd == 128) &&
-         seq < (1 << 30) && heads < (1 << 20) && batch * heads < (1 << 24);
+         seq < (1 << 30) && heads < (1 << 20) && batch * heads < (1 << 24) &&
+         (int64_t)kTile * 3 * heads * hd * 2 < (int64_t(1) << 31);
 }
 
 template <int HD>
