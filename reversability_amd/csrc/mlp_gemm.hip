@@ -843,9 +843,13 @@ int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
 
 // Weight-gradient plan for an ni x nj output reduced over `rows` tokens: tile
 // shape and split count minimising a simple cost (MFMA time at a per-shape
-// efficiency, scaled down when the grid is under one workgroup per CU, plus
-// the partial sums' HBM round trip at ~500 flop per byte).  Depends only on
-// the sizes, so results are device-independent.
+// efficiency, divided by the fraction of the grid's CU rounds that hold a
+// workgroup, plus the partial sums' HBM round trip at ~500 flop per byte).
+// The split count is the largest that keeps tiles x splits within one round
+// of the CUs: a grid a few workgroups past the CU count (C5's qkv weight
+// gradient: 96 tiles x 3 splits = 288) leaves those CUs a second turn and
+// nearly doubles the kernel.  Depends only on the sizes, so results are
+// device-independent.
 struct WgradPlan {
   int shape;
   int64_t tiles_m, tiles_n, splits, chunk;
@@ -858,7 +862,7 @@ WgradPlan plan_wgrad(int64_t rows, int64_t ni, int64_t nj) {
     const TileShape t = kShapes[i];
     if (ni % t.bm || nj % t.bn) continue;
     const int64_t tiles = (ni / t.bm) * (nj / t.bn);
-    int64_t splits = (kCUs + tiles - 1) / tiles;
+    int64_t splits = tiles >= kCUs ? 1 : kCUs / tiles;
     const int64_t max_splits = (rows + 4 * kBK - 1) / (4 * kBK);  // >= 4 stages per split
     if (splits > max_splits) splits = max_splits;
     if (splits > 64) splits = 64;
@@ -866,8 +870,9 @@ WgradPlan plan_wgrad(int64_t rows, int64_t ni, int64_t nj) {
     int64_t chunk = (rows + splits - 1) / splits;
     chunk = (chunk + kBK - 1) / kBK * kBK;
     splits = (rows + chunk - 1) / chunk;
-    const double fill = (double)(tiles * splits) / kCUs;
-    const double flops = 2.0 * rows * ni * nj / (eff[i] * (fill < 1 ? fill : 1));
+    const int64_t wgs = tiles * splits, rounds = (wgs + kCUs - 1) / kCUs;
+    const double fill = (double)wgs / (double)(rounds * kCUs);
+    const double flops = 2.0 * rows * ni * nj / (eff[i] * fill);
     const double bytes = splits > 1 ? 8.0 * splits * ni * nj : 0.0;
     const double cost = flops + 500.0 * bytes;
     if (best.shape < 0 || cost < best_cost) {
