@@ -107,10 +107,13 @@ class FusedRMSNormPass(torch.autograd.Function):
     beside the attention graph).  Backward in one pass: the norm backward plus
     the pass-through output's gradient (``rv_rmsnorm_bwd_acc``), the sum
     autograd would otherwise form in a separate kernel.  y as FusedRMSNorm's
-    (fp16 under fp16 autocast with ``fp16_out``)."""
+    (fp16 under fp16 autocast with ``fp16_out``).  ``half_grad``: a list that
+    receives fp16(x's gradient), written by the same backward pass, for a
+    caller that also needs that gradient in fp16 (the Euler reconstruction
+    hands the next layer's fp16 force its output gradient without a cast)."""
 
     @staticmethod
-    def forward(ctx, x, weight, eps, fp16_out=False, pre=None):
+    def forward(ctx, x, weight, eps, fp16_out=False, pre=None, half_grad=None):
         ctx.set_materialize_grads(False)
         if pre is None:
             half = bool(fp16_out) and _fp16_out(x, weight)
@@ -118,6 +121,7 @@ class FusedRMSNormPass(torch.autograd.Function):
         else:  # (y, rstd) already computed from x (inverse_rms_norm)
             y, rstd = pre
         ctx.save_for_backward(x, weight, rstd)
+        ctx.half_grad = half_grad
         return x.view_as(x), y
 
     @staticmethod
@@ -125,26 +129,31 @@ class FusedRMSNormPass(torch.autograd.Function):
     def backward(ctx, dpass, dy):
         x, weight, rstd = ctx.saved_tensors
         if dy is None:
-            return dpass, None, None, None, None
+            return dpass, None, None, None, None, None
         if dy.dtype not in (torch.float32, torch.float16):
             dy = dy.float()
-        dx, _, dweight = ops.rmsnorm_bwd_acc(x, weight.contiguous(), dy.contiguous(), rstd,
-                                             dpass.contiguous() if dpass is not None else None,
-                                             False)
-        return dx, dweight, None, None, None
+        want16 = ctx.half_grad is not None
+        dx, dx16, dweight = ops.rmsnorm_bwd_acc(x, weight.contiguous(), dy.contiguous(), rstd,
+                                                dpass.contiguous() if dpass is not None else None,
+                                                want16)
+        if want16:
+            ctx.half_grad.append(dx16)
+        return dx, dweight, None, None, None, None
 
 
-def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module, pre=None):
+def rms_norm_pass(x: torch.Tensor, norm: torch.nn.Module, pre=None, half_grad=None):
     """``(x', norm(x))`` with x' = x for x's other use (see FusedRMSNormPass), on the
     fused kernels when ``norm`` is routed by ``enable_rmsnorm`` and x is a
     contiguous fp32 GPU tensor whose rows the vector kernels cover; otherwise
     ``(x, norm(x))`` (also for a norm weight that is not 16-byte aligned).  ``pre``:
-    the (y, rstd) ``inverse_rms_norm`` returned for x."""
+    the (y, rstd) ``inverse_rms_norm`` returned for x.  ``half_grad``: a list
+    that the fused backward appends fp16(x's gradient) to (nothing is appended
+    on the unfused path or when the norm output gets no gradient)."""
     if (getattr(norm, "_rv_fused", False) and x.is_cuda and x.dtype == torch.float32
             and x.is_contiguous() and x.shape[-1] % 4 == 0 and x.data_ptr() % 16 == 0
             and norm.weight.is_contiguous() and norm.weight.data_ptr() % 16 == 0):
         return FusedRMSNormPass.apply(x, norm.weight, rms_norm_eps(norm, x),
-                                      getattr(norm, "_rv_fp16_out", False), pre)
+                                      getattr(norm, "_rv_fp16_out", False), pre, half_grad)
     return x, norm(x)
 
 

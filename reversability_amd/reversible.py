@@ -86,15 +86,17 @@ def _grads_in_order(block, params, grads):
     return [by_id[id(w)] for w in block.parameters()]
 
 
-def _euler_layer_vjp(block, p, q, dp, dq, settings):
+def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None):
     """Invert one Euler step -- (p, q) = (p0 + M(q), q0 + A(p0)) -- and take its
     VJP with one evaluation of each force, both with their graphs: M at the
     stored q (it inverts the step and, linearised there, serves the VJP) and
     A at the recovered p0.  The VJP runs in two phases: the MLP's, giving the
     gradient at M's input, then the step's rest (A, both norms and the
     residual sums) with that gradient entering at the rebuilt q0 + A(p0).
-    Returns (p0, q0, dp0, dq0, parameter gradients in block.parameters()
-    order)."""
+    ``dp16``: fp16(dp) if the caller has it (the layer above's p0 gradient,
+    written by its norm backward), handed to an fp16 force as is -- the value
+    autograd's cast of dp would give.  Returns (p0, q0, dp0, dq0, parameter
+    gradients in block.parameters() order, fp16(dp0) or None)."""
     # the states may be the stack's own saved outputs: nothing here may extend
     # their history (a graph reaching the stack node would re-enter its backward)
     p, q = p.detach(), q.detach()
@@ -113,9 +115,10 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings):
             p0, pre_p0 = inverse_rms_norm(p, force.detach(), block.attn_norm)
         else:
             p0, pre_p0 = euler_step(p, force.detach(), -1), None
+    half_dp0: list = []  # fp16(dp0), from p0's norm backward when the fused path runs
     with torch.enable_grad():
         p0 = p0.detach().requires_grad_(True)
-        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0)
+        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0, half_dp0)
         attention = block.attn(normed_p0)
     with torch.no_grad():
         q0 = euler_step(q, attention.detach(), -1)
@@ -124,7 +127,8 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings):
                                                               *block.mlp.parameters())
     attn_params = (*block.attn_norm.parameters(), *block.attn.parameters())
     with torch.enable_grad():
-        first = torch.autograd.grad(force, (m_in, *mlp_params), dp)
+        grad_force = dp16 if dp16 is not None and force.dtype == torch.float16 else dp
+        first = torch.autograd.grad(force, (m_in, *mlp_params), grad_force)
         del force
         if fused:  # next_q = q0 + A(p0) carrying the value q and its norm
             next_q, y = FusedAddRMSNorm.apply(q0, attention, block.mlp_norm.weight,
@@ -139,7 +143,8 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings):
             rest = torch.autograd.grad((next_q, p0_pass), (p0, q0, *attn_params),
                                        (dq + first[0], dp))
             grads = _grads_in_order(block, (*attn_params, *mlp_params), (*rest[2:], *first[1:]))
-    return p0.detach(), q0.detach(), rest[0], rest[1], grads
+    return (p0.detach(), q0.detach(), rest[0], rest[1], grads,
+            half_dp0[0] if half_dp0 else None)
 
 
 def _euler_inverse_for_vjp(block, p, q, settings):
@@ -206,11 +211,14 @@ class _InverseStack(torch.autograd.Function):
         # skipping the cache changes no value.
         with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype,
                             cache_enabled=False), eager_updates(ctx.eager):
+            dp16 = None
             for block in reversed(ctx.blocks):
                 if ctx.method == "euler" and settings.euler_mlp_at_stored_q:
-                    p, q, dp, dq, layer = _euler_layer_vjp(block, p, q, dp, dq, settings)
+                    p, q, dp, dq, layer, dp16 = _euler_layer_vjp(block, p, q, dp, dq, settings,
+                                                                 dp16)
                     grads[0:0] = layer
                     continue
+                dp16 = None
                 if ctx.method == "euler" and settings.reuse_euler_attention:
                     next_p, next_q, p0, q0 = _euler_inverse_for_vjp(block, p, q, settings)
                 else:

@@ -444,7 +444,9 @@ def test_rmsnorm_pass_matches_composition(cuda_device, rows, width, fp16_out):
     """FusedRMSNormPass = the norm + autograd's sum of x's two gradients (the
     norm's and the pass-through use's): y, dx bit for bit; dweight too except
     at width > 256 (the accumulating backward's 4 waves per block sum the
-    same per-row terms in another fixed order: within fp32 summation error)."""
+    same per-row terms in another fixed order: within fp32 summation error).
+    The fp16 copy of dx it hands a ``half_grad`` list is dx's cast, bit for
+    bit."""
     from reversability_amd.kernels_v3 import FusedRMSNormPass
     g = torch.Generator().manual_seed(rows * 3 + width)
     x0 = torch.randn(rows, width, generator=g).to(cuda_device)
@@ -453,11 +455,12 @@ def test_rmsnorm_pass_matches_composition(cuda_device, rows, width, fp16_out):
     gp = torch.randn(rows, width, generator=g).to(cuda_device)
     eps = float(torch.finfo(torch.float32).eps)
     outs = []
+    half: list = []
     for fused in (True, False):
         x, w = x0.clone().requires_grad_(True), w0.clone().requires_grad_(True)
         with torch.autocast("cuda", dtype=torch.float16, enabled=fp16_out):
             if fused:
-                xp, y = FusedRMSNormPass.apply(x, w, eps, fp16_out)
+                xp, y = FusedRMSNormPass.apply(x, w, eps, fp16_out, None, half)
             else:
                 xp, y = x, FusedRMSNorm.apply(x, w, eps, fp16_out)
         loss = (y.float() * gy).sum() + (xp * gp).sum()
@@ -465,6 +468,8 @@ def test_rmsnorm_pass_matches_composition(cuda_device, rows, width, fp16_out):
         outs.append((y.detach(), x.grad, w.grad))
     (y1, dx1, dw1), (y2, dx2, dw2) = outs
     assert torch.equal(y1, y2) and torch.equal(dx1, dx2)
+    assert len(half) == 1 and half[0].dtype == torch.float16
+    assert torch.equal(half[0], dx1.half())
     if width > 256:
         assert torch.allclose(dw1, dw2, rtol=1e-5, atol=1e-6)
     else:
