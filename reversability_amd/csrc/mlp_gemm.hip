@@ -625,7 +625,20 @@ void wgrad_reduce(ReduceSeg a, ReduceSeg b, int accumulate) {
   const int64_t i = (blk * 256 + threadIdx.x) * 4;
   if (i >= n) return;
   float4 s = *reinterpret_cast<const float4*>(part + i);
-  for (int k = 1; k < splits; ++k) {
+  // the partials of eight splits loaded before the first of their adds (one
+  // memory round trip per eight splits instead of per split); same order
+  int k = 1;
+  for (; k + 8 <= splits; k += 8) {
+    float4 t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      t[j] = *reinterpret_cast<const float4*>(part + (int64_t)(k + j) * n + i);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s.x = s.x + t[j].x; s.y = s.y + t[j].y; s.z = s.z + t[j].z; s.w = s.w + t[j].w;
+    }
+  }
+  for (; k < splits; ++k) {
     const float4 t = *reinterpret_cast<const float4*>(part + (int64_t)k * n + i);
     s.x = s.x + t.x; s.y = s.y + t.y; s.z = s.z + t.z; s.w = s.w + t.w;
   }
