@@ -56,6 +56,26 @@ def forward_pair(block, p, q, method, h):
     return euler_step(p, block.mlp(normed), +1), next_q
 
 
+def euler_forward(blocks, p, q):
+    """forward_pair's Euler steps over a stack, each p' = p + M(q') made in one
+    pass with the next block's attn_norm(p') (add_rms_norm: the residual add
+    and the norm where the fused kernels apply, else the add and the norm), so
+    the next block reads its normalized input instead of normalizing p' again.
+    The same values as calling forward_pair block by block."""
+    normed = None
+    for i, block in enumerate(blocks):
+        if normed is None:
+            normed = block.attn_norm(p)
+        next_q, mlp_in = add_rms_norm(q, block.attn(normed), block.mlp_norm)
+        force = block.mlp(mlp_in)
+        if i + 1 < len(blocks):
+            p, normed = add_rms_norm(p, force, blocks[i + 1].attn_norm)
+        else:
+            p = euler_step(p, force, +1)
+        q = next_q
+    return p, q
+
+
 def inverse_pair(block, p, q, method, h):
     """Algebraic inverse of forward_pair (reversible.py:28-32)."""
     if method == "midpoint":
@@ -115,10 +135,13 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None):
             p0, pre_p0 = inverse_rms_norm(p, force.detach(), block.attn_norm)
         else:
             p0, pre_p0 = euler_step(p, force.detach(), -1), None
-    half_dp0: list = []  # fp16(dp0), from p0's norm backward when the fused path runs
+    # fp16(dp0) from p0's norm backward when the fused path runs, for the lower
+    # layer's force -- fp16 like this one's (asked only then)
+    half_dp0: list = []
     with torch.enable_grad():
         p0 = p0.detach().requires_grad_(True)
-        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0, half_dp0)
+        p0_pass, normed_p0 = rms_norm_pass(p0, block.attn_norm, pre_p0,
+                                           half_dp0 if force.dtype == torch.float16 else None)
         attention = block.attn(normed_p0)
     with torch.no_grad():
         q0 = euler_step(q, attention.detach(), -1)
@@ -193,8 +216,11 @@ class _InverseStack(torch.autograd.Function):
         ctx.device_type = p.device.type
         ctx.amp_enabled = torch.is_autocast_enabled(ctx.device_type)
         ctx.amp_dtype = torch.get_autocast_dtype(ctx.device_type)
-        for block in blocks:
-            p, q = forward_pair(block, p, q, method, h)
+        if method == "euler":
+            p, q = euler_forward(blocks, p, q)
+        else:
+            for block in blocks:
+                p, q = forward_pair(block, p, q, method, h)
         ctx.save_for_backward(p, q, *parameters)
         return p, q
 

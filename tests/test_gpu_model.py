@@ -456,6 +456,30 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_euler_forward_with_next_norm_bitwise(cuda_device, fused):
+    """The Euler stack's forward with each p' = p + M(q') made together with the
+    next block's attention norm (euler_forward) returns the same (p, q), bit for
+    bit, as forward_pair block by block: on the fused fp16-output norms at
+    width 1024 (the configs[4] wiring), and on the plain fp32 path."""
+    from reversability_amd.reversible import euler_forward
+    torch.manual_seed(17)
+    cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3, "n_heads": 16,
+                     "d_model": 1024, "d_ff": 2048}, "method": "euler", "step_size": 0.5}
+    model = build_model(cfg).to(cuda_device)
+    if fused:
+        install_v3(model, core_mode="reference", mlp_tokens=512, swiglu=True, rmsnorm=True)
+        enable_linear(model)
+        enable_attention(model)
+    x = torch.randn(2, 256, 1024, device=cuda_device)
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16, enabled=fused):
+        p1, q1 = euler_forward(model.blocks, x, x)
+        p2, q2 = x, x
+        for block in model.blocks:
+            p2, q2 = forward_pair(block, p2, q2, "euler", 0.5)
+    assert torch.equal(p1, p2) and torch.equal(q1, q2)
+
+
 def test_split_midpoint_fused_update_norm_bitwise(cuda_device):
     """The split midpoint core with each midpoint update made together with
     the next layer's attention norm (fuse_midpoint_norm) gives the same loss
