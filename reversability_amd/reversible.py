@@ -106,7 +106,7 @@ def _grads_in_order(block, params, grads):
     return [by_id[id(w)] for w in block.parameters()]
 
 
-def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None):
+def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None, lower=None, pre_q=None):
     """Invert one Euler step -- (p, q) = (p0 + M(q), q0 + A(p0)) -- and take its
     VJP with one evaluation of each force, both with their graphs: M at the
     stored q (it inverts the step and, linearised there, serves the VJP) and
@@ -115,16 +115,20 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None):
     residual sums) with that gradient entering at the rebuilt q0 + A(p0).
     ``dp16``: fp16(dp) if the caller has it (the layer above's p0 gradient,
     written by its norm backward), handed to an fp16 force as is -- the value
-    autograd's cast of dp would give.  Returns (p0, q0, dp0, dq0, parameter
-    gradients in block.parameters() order, fp16(dp0) or None)."""
+    autograd's cast of dp would give.  ``lower``: the block below, whose M
+    input -- its mlp_norm of q0 -- is made with q0 = q - A(p0) in one pass
+    when ``fuse_euler_inverse`` is set and the fused norms apply; ``pre_q``:
+    that (y, rstd) of this block's q, made by the layer above.  Returns (p0,
+    q0, dp0, dq0, parameter gradients in block.parameters() order, fp16(dp0)
+    or None, the (y, rstd) for ``lower`` or None)."""
     # the states may be the stack's own saved outputs: nothing here may extend
     # their history (a graph reaching the stack node would re-enter its backward)
     p, q = p.detach(), q.detach()
     fused = _fp16_norm_input(block.mlp_norm, q)
     with torch.enable_grad():
         if fused:  # M's input is the fp16 norm of the stored q (graph from its leaf)
-            y_q, rstd_q = ops.rmsnorm_fwd(q, block.mlp_norm.weight.contiguous(),
-                                          rms_norm_eps(block.mlp_norm, q), True)
+            y_q, rstd_q = pre_q if pre_q is not None else ops.rmsnorm_fwd(
+                q, block.mlp_norm.weight.contiguous(), rms_norm_eps(block.mlp_norm, q), True)
             m_in = y_q.requires_grad_(True)
             force = block.mlp(m_in)
         else:  # M's input is the stored state itself
@@ -144,7 +148,10 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None):
                                            half_dp0 if force.dtype == torch.float16 else None)
         attention = block.attn(normed_p0)
     with torch.no_grad():
-        q0 = euler_step(q, attention.detach(), -1)
+        if settings.fuse_euler_inverse and lower is not None:
+            q0, pre_lower = inverse_rms_norm(q, attention.detach(), lower.mlp_norm)
+        else:
+            q0, pre_lower = euler_step(q, attention.detach(), -1), None
     q0.requires_grad_(True)
     mlp_params = tuple(block.mlp.parameters()) if fused else (*block.mlp_norm.parameters(),
                                                               *block.mlp.parameters())
@@ -167,7 +174,7 @@ def _euler_layer_vjp(block, p, q, dp, dq, settings, dp16=None):
                                        (dq + first[0], dp))
             grads = _grads_in_order(block, (*attn_params, *mlp_params), (*rest[2:], *first[1:]))
     return (p0.detach(), q0.detach(), rest[0], rest[1], grads,
-            half_dp0[0] if half_dp0 else None)
+            half_dp0[0] if half_dp0 else None, pre_lower)
 
 
 def _euler_inverse_for_vjp(block, p, q, settings):
@@ -237,14 +244,16 @@ class _InverseStack(torch.autograd.Function):
         # skipping the cache changes no value.
         with torch.autocast(ctx.device_type, enabled=ctx.amp_enabled, dtype=ctx.amp_dtype,
                             cache_enabled=False), eager_updates(ctx.eager):
-            dp16 = None
-            for block in reversed(ctx.blocks):
+            dp16 = pre_q = None
+            for index in reversed(range(len(ctx.blocks))):
+                block = ctx.blocks[index]
                 if ctx.method == "euler" and settings.euler_mlp_at_stored_q:
-                    p, q, dp, dq, layer, dp16 = _euler_layer_vjp(block, p, q, dp, dq, settings,
-                                                                 dp16)
+                    lower = ctx.blocks[index - 1] if index > 0 else None
+                    p, q, dp, dq, layer, dp16, pre_q = _euler_layer_vjp(
+                        block, p, q, dp, dq, settings, dp16, lower, pre_q)
                     grads[0:0] = layer
                     continue
-                dp16 = None
+                dp16 = pre_q = None
                 if ctx.method == "euler" and settings.reuse_euler_attention:
                     next_p, next_q, p0, q0 = _euler_inverse_for_vjp(block, p, q, settings)
                 else:

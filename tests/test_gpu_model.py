@@ -456,6 +456,35 @@ def test_euler_unused_mlp_output_skipped_bitwise(cuda_device, keep_tiles, switch
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("width,heads", [(256, 4), (1024, 16)])
+def test_euler_stored_q_fused_inverse_bitwise(cuda_device, width, heads):
+    """The Euler VJP at the stored state with fuse_euler_inverse -- p0 made with
+    its attention norm, and q0 = q - A(p0) made with the lower block's MLP norm
+    (that block's M input) -- gives the loss and every gradient bit for bit as
+    the unfused subtractions and norms."""
+    torch.manual_seed(19)
+    cfg = {"model": {"vocab_size": 512, "max_sequence_length": 256, "n_layers": 3,
+                     "n_heads": heads, "d_model": width, "d_ff": 2 * width},
+           "method": "euler", "step_size": 0.5}
+    model = build_model(cfg).to(cuda_device)
+    install_v3(model, core_mode="reference", mlp_tokens=512, swiglu=True, rmsnorm=True,
+               keep_mlp_tiles=True)
+    enable_linear(model)
+    enable_attention(model)
+    ids = torch.randint(0, 512, (2, 256), device=cuda_device)
+    runs = []
+    for on in (False, True):
+        paths.configure(model, fuse_euler_inverse=on, euler_mlp_at_stored_q=True)
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = F.cross_entropy(model(ids).flatten(0, 1).float(), ids.flatten())
+        loss.backward()
+        runs.append((loss.detach(), [p.grad.clone() for p in model.parameters()]))
+    assert torch.equal(runs[0][0], runs[1][0])
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("fused", [True, False])
 def test_euler_forward_with_next_norm_bitwise(cuda_device, fused):
     """The Euler stack's forward with each p' = p + M(q') made together with the
