@@ -21,13 +21,15 @@
 // does not cross run a code path without masking.
 // lse = m + log2 l (base-2 units) is kept for the backward.
 //
-// Backward (FA2 order, no atomics, deterministic):
-//   delta = rowsum(dO * O)                                  attn_bwd_pre_k
+// Backward (FA2 order, no atomics, deterministic), two launches:
+//   dQ: one workgroup = 128 queries; key tiles streamed; each lane first
+//     forms its query's delta = rowsum(dO * O) from the dO and O fragments it
+//     holds (its half of the row, then the other half from lane l ^ 32) and
+//     writes it for the next kernel; then
+//     S^T, dP^T (queries in lanes), dQ^T += K^T dS^T           attn_bwd_q_k
 //   dK, dV: one workgroup = 128 keys; query tiles of 64 streamed; per wave
 //     S = Q K^T, dP = dO V^T (keys in lanes), P = 2^(S c - lse),
 //     dS = P (dP - delta), dV^T += dO^T P, dK^T += Q^T dS      attn_bwd_kv_k
-//   dQ: one workgroup = 128 queries; key tiles streamed;
-//     S^T, dP^T (queries in lanes), dQ^T += K^T dS^T           attn_bwd_q_k
 //   dK and dQ are multiplied by the scale once, at the end.
 //
 // MFMA operand layout (gfx950, 32x32x16 f16): mfma(X, Y, acc) takes 8
@@ -370,29 +372,6 @@ void attn_fwd_k(const __half* __restrict__ qkv, __half* __restrict__ out, float*
 // ---------------------------------------------------------------------------
 // Backward.
 // ---------------------------------------------------------------------------
-// delta[bh][t] = sum_d dout[b][t][h][d] * out[b][t][h][d] (fp32, d in order).
-template <int HD>
-__global__ __launch_bounds__(kThreads)
-void attn_bwd_pre_k(const __half* __restrict__ out, const __half* __restrict__ dout,
-                    float* __restrict__ delta, int T, int H, int64_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // (b, t, h) row
-  if (r >= rows) return;
-  const __half* o = out + r * HD;
-  const __half* g = dout + r * HD;
-  float acc = 0.f;
-#pragma unroll
-  for (int c8 = 0; c8 < HD / 8; ++c8) {
-    const f16x8 ov = *reinterpret_cast<const f16x8*>(o + c8 * 8);
-    const f16x8 gv = *reinterpret_cast<const f16x8*>(g + c8 * 8);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc = fmaf((float)gv[i], (float)ov[i], acc);
-  }
-  const int64_t bt = r / H;
-  const int h = (int)(r % H);
-  const int64_t b = bt / T, t = bt % T;
-  delta[(b * H + h) * T + t] = acc;
-}
-
 // dK/dV contribution of 32 staged queries (tile rows r0 .. r0 + 31 of Q / dO)
 // to one wave's 32 keys (lanes).  MASK: the causal diagonal crosses the pair;
 // tile row r is visible to the lane's key iff r >= krel = key - (first query
@@ -588,9 +567,10 @@ void attn_bwd_kv_k(const __half* __restrict__ qkv, const __half* __restrict__ do
 
 template <int HD>
 __global__ __launch_bounds__(kThreads, kMinBlocks<HD>)
-void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ dout,
-                  const float* __restrict__ lse, const float* __restrict__ delta,
-                  __half* __restrict__ dqkv, int T, int H, int n_qt, float c, float scale) {
+void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ out,
+                  const __half* __restrict__ dout, const float* __restrict__ lse,
+                  float* __restrict__ delta, __half* __restrict__ dqkv, int T, int H, int n_qt,
+                  float c, float scale) {
   constexpr int KK = HD / 16, DT = HD / 32;
   __shared__ __attribute__((aligned(16))) _Float16 lds[2][2][kTile * HD];  // [buf][K / V]
   const int BH = (int)(gridDim.x / n_qt);
@@ -616,7 +596,22 @@ void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ dou
                  : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   const float Lq = qok ? lse[(int64_t)bh * T + q] : 0.f;
-  const float Dq = qok ? delta[(int64_t)bh * T + q] : 0.f;
+  // delta = sum_d dO O over the query's row: this lane's HD / 2 columns (the
+  // fragments' layout), then the other half from lane l ^ 32
+  float dsum = 0.f;
+  {
+    const __half* ob = out + (int64_t)b * T * os + (int64_t)h * HD;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const f16x8 of = qok ? *reinterpret_cast<const f16x8*>(ob + (int64_t)q * os + kk * 16 +
+                                                             hl * 8)
+                           : f16x8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dsum = fmaf((float)gf[kk][i], (float)of[i], dsum);
+    }
+  }
+  const float Dq = pair_sum(dsum);
+  if (qok && hl == 0) delta[(int64_t)bh * T + q] = Dq;
   f32x16 dq[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) dq[dt] = zero16();
@@ -693,19 +688,16 @@ int launch_fwd(const __half* qkv, int64_t B, int64_t T, int64_t H, __half* out, 
 template <int HD>
 int launch_bwd(const __half* qkv, const __half* out, const __half* dout, const float* lse,
                int64_t B, int64_t T, int64_t H, __half* dqkv, float* delta, hipStream_t s) {
-  const int64_t rows = B * T * H;
-  hipLaunchKernelGGL(attn_bwd_pre_k<HD>, dim3((unsigned)((rows + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, s, out, dout, delta, (int)T, (int)H, rows);
-  int rc = rv_host::check_launch();
-  if (rc != RV_OK) return rc;
   const int n_t = (int)((T + kBlockRows - 1) / kBlockRows);
   const double scale = 1.0 / std::sqrt((double)HD);
   const float c = (float)(1.4426950408889634 * scale);
   const dim3 grid((unsigned)(n_t * B * H));
+  // the dQ kernel writes delta, which the dK/dV kernel reads
+  hipLaunchKernelGGL(attn_bwd_q_k<HD>, grid, dim3(kThreads), 0, s, qkv, out, dout, lse, delta,
+                     dqkv, (int)T, (int)H, n_t, c, (float)scale);
+  int rc = rv_host::check_launch();
+  if (rc != RV_OK) return rc;
   hipLaunchKernelGGL(attn_bwd_kv_k<HD>, grid, dim3(kThreads), 0, s, qkv, dout, lse, delta, dqkv,
-                     (int)T, (int)H, n_t, c, (float)scale);
-  if ((rc = rv_host::check_launch()) != RV_OK) return rc;
-  hipLaunchKernelGGL(attn_bwd_q_k<HD>, grid, dim3(kThreads), 0, s, qkv, dout, lse, delta, dqkv,
                      (int)T, (int)H, n_t, c, (float)scale);
   return rv_host::check_launch();
 }
