@@ -482,13 +482,17 @@ void gemm_kernel(GemmArgs args) {
         const u32x4 gw = *reinterpret_cast<const u32x4*>(stage + r * S + c * 8);
         const u32x4 vw = *reinterpret_cast<const u32x4*>(stage + r * S + WN / 2 + c * 8);
         const __half* gh = reinterpret_cast<const __half*>(&gw);
-        const __half* vh = reinterpret_cast<const __half*>(&vw);
-        __half oh[8];
+        const __half2* vh2 = reinterpret_cast<const __half2*>(&vw);
+        // silu rounded to fp16, times v: the exact product of two fp16 values
+        // rounded once, so the packed fp16 multiply gives the fp32 expression's
+        // bits two values per instruction
+        __half2 oh[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float g = __half2float(gh[e]);
-          const float silu = rv::round_to<__half>(g * rv::fast_sigmoid(g));
-          oh[e] = __float2half_rn(silu * __half2float(vh[e]));
+        for (int e = 0; e < 4; ++e) {
+          const float g0 = __half2float(gh[2 * e]), g1 = __half2float(gh[2 * e + 1]);
+          const __half2 silu = __floats2half2_rn(g0 * rv::fast_sigmoid(g0),
+                                                 g1 * rv::fast_sigmoid(g1));
+          oh[e] = __hmul2(silu, vh2[e]);
         }
         __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(oh), reinterpret_cast<u32x4*>(static_cast<__half*>(args.c) + row * args.ldc + col));
         if (u != nullptr) {
@@ -536,20 +540,21 @@ void gemm_kernel(GemmArgs args) {
           const int64_t row = row0 + r;
           if (row < args.m) {
             const u32x4 dw = *reinterpret_cast<const u32x4*>(stage + r * S + c * 8);
-            const __half* dh = reinterpret_cast<const __half*>(&dw);
+            const __half2* dh2 = reinterpret_cast<const __half2*>(&dw);
             const __half* gh = reinterpret_cast<const __half*>(&gw[i]);
-            const __half* vh = reinterpret_cast<const __half*>(&vw[i]);
-            __half dgo[8], dvo[8];
+            const __half2* vh2 = reinterpret_cast<const __half2*>(&vw[i]);
+            // d*v and d*silu are products of two fp16 values rounded to fp16
+            // once: packed fp16 multiplies, the same bits as the fp32 forms
+            __half2 dgo[4], dvo[4];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float d = __half2float(dh[e]);
-              const float g = __half2float(gh[e]);
-              const float v = __half2float(vh[e]);
-              const float sg = rv::fast_sigmoid(g);
-              const float silu = rv::round_to<__half>(g * sg);
-              const float dgi = rv::round_to<__half>(d * v);
-              dgo[e] = __float2half_rn(dgi * (sg * (1.0f + g * (1.0f - sg))));
-              dvo[e] = __float2half_rn(d * silu);
+            for (int e = 0; e < 4; ++e) {
+              const float g0 = __half2float(gh[2 * e]), g1 = __half2float(gh[2 * e + 1]);
+              const float s0 = rv::fast_sigmoid(g0), s1 = rv::fast_sigmoid(g1);
+              const __half2 silu = __floats2half2_rn(g0 * s0, g1 * s1);
+              const __half2 dgi = __hmul2(dh2[e], vh2[e]);
+              dgo[e] = __floats2half2_rn(__low2float(dgi) * (s0 * (1.0f + g0 * (1.0f - s0))),
+                                         __high2float(dgi) * (s1 * (1.0f + g1 * (1.0f - s1))));
+              dvo[e] = __hmul2(dh2[e], silu);
             }
             __half* du = static_cast<__half*>(args.c) + row * args.ldc;
             __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(dgo), reinterpret_cast<u32x4*>(du + col));
