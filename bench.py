@@ -822,7 +822,7 @@ def main() -> int:
         line["attention"] = attention_bench(dev)
         line["embedding"] = embedding_bench(dev)
         line["train_step"] = train_step_bench(dev, args.train_steps, args.train_warmup)
-        line["train_step_c5"] = train_step_bench(dev, 5, 2, "c5")
+        line["train_step_c5"] = train_step_bench(dev, args.train_steps, args.train_warmup, "c5")
         if args.cpu_seconds > 0:
             line["train_step"]["cpu_baseline"] = cpu_train_baseline(args.cpu_seconds)
     if args.cpu_seconds > 0:
