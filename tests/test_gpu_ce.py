@@ -168,7 +168,7 @@ def _same_bits(a, b):
     (64, 50257, 50304, 0),     # the tied head's padded stride
     (37, 50257, 50257, 0),     # odd stride: every row has a scalar head and tail
     (19, 65536, 65536, 0),     # widest row the registers hold
-    (11, 65535, 65536, 3),     # misaligned base, 32 vectors per thread
+    (11, 65535, 65536, 3),     # misaligned base, 16 vectors per thread
     (23, 2048, 2051, 5),
     (9, 7, 8, 1),              # no vector part
     (5, 1, 1, 0),
