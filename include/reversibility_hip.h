@@ -379,7 +379,7 @@ int rv_adamw_step_clipped(int count, float* const* params, const float* const* g
 
 /* GradScaler.unscale_ followed by torch.nn.utils.clip_grad_norm_(params,
  * max_norm) (norm type 2; scripts/train_baseline.py:278-280) without writing
- * the gradients: rv_grad_sq_partials stores, for each 65536-element chunk of
+ * the gradients: rv_grad_sq_partials stores, for each 16384-element chunk of
  * each of count <= rv_adamw_max_tensors() gradients, the fp32 sum of squares
  * of g * *inv_scale (inv_scale nullable) and a non-finite flag at index
  * first + chunk of partials / flags (rv_grad_chunks(numel, count) chunks; a

@@ -161,7 +161,7 @@ def test_multi_cast_validates_without_device():
 def test_grad_clip_entry_points_validate_without_device():
     lib = _hip.library()
     fake = ctypes.c_void_p(4096)
-    n = (ctypes.c_int64 * 3)(65536, 65537, 1)
+    n = (ctypes.c_int64 * 3)(16384, 16385, 1)  # 16384-element chunks
     assert lib.rv_grad_chunks(n, 3) == 1 + 2 + 1
     assert lib.rv_grad_chunks(n, 0) == 0
     assert lib.rv_grad_chunks(n, -1) < 0
