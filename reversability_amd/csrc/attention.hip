@@ -179,6 +179,15 @@ __device__ __forceinline__ float pair_sum(float v) {
 // first row (l/32)*4: (j/4)*8 + j%4.
 __device__ __forceinline__ constexpr int acc_row(int j) { return (j >> 2) * 8 + (j & 3); }
 
+// Wave priorities inside one SIMD: a wave issues its score MFMA chains (S,
+// and dP in the backward) at priority 2, the forward's P V chain at 1 and its
+// softmax arithmetic at 0, so that the instruction arbiter prefers the wave
+// with matrix work ready and the other waves' exponentials fill the matrix
+// core's gaps (C5 forward 214-219 -> 208 us, backward -1%; results unchanged).
+__device__ __forceinline__ void prio_mfma() { __builtin_amdgcn_s_setprio(2); }
+__device__ __forceinline__ void prio_mfma_tail() { __builtin_amdgcn_s_setprio(1); }
+__device__ __forceinline__ void prio_valu() { __builtin_amdgcn_s_setprio(0); }
+
 // The running max is moved only when a score exceeds it by more than kLazy
 // (base-2 units): p = 2^(S c - m) then stays below 2^kLazy (exact in fp16's
 // exponent range), and the rescale of o and l is skipped on most tiles.
@@ -237,6 +246,7 @@ __device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, c
   constexpr int KK = HD / 16, DT = HD / 32;
   const int hl = lane >> 5;
   f32x16 s[2];
+  prio_mfma();
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     if (sub == 1 && MASK && !live1) break;
@@ -245,6 +255,7 @@ __device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, c
     for (int kk = 1; kk < KK; ++kk) s[sub] = mfma(fo.rowf(Ks, sub, kk), qf[kk], s[sub]);
   }
   const bool two = !MASK || live1;
+  prio_valu();
   float mx = -INFINITY;
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
@@ -273,6 +284,7 @@ __device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, c
   for (int sub = 0; sub < 2; ++sub) {
     if (sub == 1 && !two) break;
     float rowsum = 0.f;
+    prio_valu();
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float p = __builtin_amdgcn_exp2f(fmaf(s[sub][j], c, neg_m));
@@ -280,6 +292,7 @@ __device__ __forceinline__ void fwd_tile(FwdState<HD>& st, const _Float16* Ks, c
       s[sub][j] = p;
     }
     st.l += rowsum;
+    prio_mfma_tail();
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
       const f16x8 pf = pack8(s[sub], cc);
@@ -387,6 +400,7 @@ __device__ __forceinline__ void kv_rows(f32x16 (&dk)[HD / 32], f32x16 (&dv)[HD /
   constexpr int KK = HD / 16, DT = HD / 32;
   const int hl = lane >> 5;
   const int sub = r0 / 32;
+  prio_mfma();
   f32x16 s = mfma(fo.rowf(Qs, sub, 0), kf[0], zero16());
   f32x16 dp = mfma(fo.rowf(Gs, sub, 0), vf[0], zero16());
 #pragma unroll
@@ -394,6 +408,7 @@ __device__ __forceinline__ void kv_rows(f32x16 (&dk)[HD / 32], f32x16 (&dv)[HD /
     s = mfma(fo.rowf(Qs, sub, kk), kf[kk], s);
     dp = mfma(fo.rowf(Gs, sub, kk), vf[kk], dp);
   }
+  prio_valu();
 #pragma unroll
   for (int jg = 0; jg < 4; ++jg) {
     const int r4 = r0 + jg * 8 + hl * 4;
@@ -435,6 +450,7 @@ __device__ __forceinline__ void q_rows(f32x16 (&dq)[HD / 32], const _Float16* Ks
   constexpr int KK = HD / 16, DT = HD / 32;
   const int hl = lane >> 5;
   const int sub = r0 / 32;
+  prio_mfma();
   f32x16 s = mfma(fo.rowf(Ks, sub, 0), qf[0], zero16());
   f32x16 dp = mfma(fo.rowf(Vs, sub, 0), gf[0], zero16());
 #pragma unroll
@@ -443,6 +459,7 @@ __device__ __forceinline__ void q_rows(f32x16 (&dq)[HD / 32], const _Float16* Ks
     dp = mfma(fo.rowf(Vs, sub, kk), gf[kk], dp);
   }
   const float neg_l = -Lq;
+  prio_valu();
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     float p = __builtin_amdgcn_exp2f(fmaf(s[j], c, neg_l));
