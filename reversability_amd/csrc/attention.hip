@@ -71,6 +71,11 @@ constexpr int kMinBlocks = HD == 128 ? 1 : 2;
 // The forward keeps fewer live registers: three workgroups per CU at HD = 64.
 template <int HD>
 constexpr int kFwdMinBlocks = HD == 128 ? 1 : (HD == 64 ? 3 : 2);
+// So does the dQ kernel: at HD = 64 three workgroups per CU fit in 168
+// registers with two spilled outside the key loop (C5 backward 652-658 ->
+// 633-638 us against two workgroups at 176 registers).
+template <int HD>
+constexpr int kQMinBlocks = HD == 128 ? 1 : (HD == 64 ? 3 : 2);
 
 template <int HD>
 __device__ __forceinline__ int swz(int r, int c) {
@@ -583,7 +588,7 @@ void attn_bwd_kv_k(const __half* __restrict__ qkv, const __half* __restrict__ do
 }
 
 template <int HD>
-__global__ __launch_bounds__(kThreads, kMinBlocks<HD>)
+__global__ __launch_bounds__(kThreads, kQMinBlocks<HD>)
 void attn_bwd_q_k(const __half* __restrict__ qkv, const __half* __restrict__ out,
                   const __half* __restrict__ dout, const float* __restrict__ lse,
                   float* __restrict__ delta, __half* __restrict__ dqkv, int T, int H, int n_qt,
