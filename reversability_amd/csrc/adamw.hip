@@ -194,7 +194,23 @@ void grad_clip_k(const float* __restrict__ part, const float* __restrict__ flag,
                  float* __restrict__ found_inf) {
   float ss = 0.f;
   float any = 0.f;
-  for (int i = threadIdx.x; i < n; i += kThreads) {
+  // each thread's partials in the same order as one at a time, loaded eight
+  // at a time (C5's 15583 partials: one memory round trip per eight)
+  int i = threadIdx.x;
+  for (; i + 7 * kThreads < n; i += 8 * kThreads) {
+    float p[8], f[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p[j] = part[i + j * kThreads];
+      f[j] = flag[i + j * kThreads];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ss = ss + p[j];
+      any = fmaxf(any, f[j]);
+    }
+  }
+  for (; i < n; i += kThreads) {
     ss = ss + part[i];
     any = fmaxf(any, flag[i]);
   }
