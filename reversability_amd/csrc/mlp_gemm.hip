@@ -467,7 +467,10 @@ void gemm_kernel(GemmArgs args) {
           p.y = *reinterpret_cast<const uint32_t*>(&h23);
           *reinterpret_cast<uint2*>(stage + (i * 32 + (lane & 31)) * S + j * 32 + q * 8 + cq) = p;
         }
-    __syncthreads();
+    // each wave reads back only its own staged block: a wave-local wait
+    // instead of a workgroup barrier, so a wave stores as soon as it has staged
+    lds_wait_all();
+    __builtin_amdgcn_wave_barrier();
     const int64_t row0 = m0 + wm * WM;
     if constexpr (EPI == Epi::SwiGLU) {
       // gate in staged columns [0, WN/2), value in [WN/2, WN)
