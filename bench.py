@@ -25,11 +25,19 @@ Also reported, on the same line:
                 of a HIP graph of back-to-back launches of that kernel),
                 against the 8 TB/s HBM peak; ``traffic`` is the HBM bytes per
                 launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs
-                (profiles/traffic.json), if recorded.
+                (profiles/traffic.json) when the kernel's sources are the ones
+                it was measured on (``traffic_measured_on``), else null.
   kernels       the same per-kernel timing for every kernel of the step
                 (rms_bwd includes its small dw-reduce launch).
+  stream_floor  per kernel, the fastest hand-written streaming kernel
+                (rv_stream_floor) moving the same arrays' bytes with the same
+                read/write shape, swept over vectors per thread and cache
+                hints; the RMSNorm backward's bytes also followed by an empty
+                launch (the floor of a two-launch backward); configs[0]'s
+                forward and backward arrays in one kernel; the step's sum.
   mlp_block     configs[2]: RMSNorm + tiled SwiGLU MLP block fwd+bwd, GEMM
-                TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak.
+                TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak and
+                algorithmic HBM GB/s (mlp_block_bytes) against 8 TB/s.
   mlp_gemms     each MFMA MLP GEMM entry point alone at one 8192-token tile
                 of configs[2] and of configs[4], TFLOP/s and peak fraction.
   train_step    configs[3]: midpoint-reversible 7-layer decoder step
@@ -46,11 +54,14 @@ Also reported, on the same line:
                 for RMSNorm fwd, add (2 reads, 1 write) for RMSNorm bwd and
                 SwiGLU fwd, mul over tensors of SwiGLU bwd's total bytes for
                 SwiGLU bwd; per kernel and for the whole step.
-  cpu_baseline  the CPU oracle (oracle/kernels_ref.c, OpenMP) on the host's
-                cores: the same RMSNorm + SwiGLU step, in GB/s.  The train
-                step carries its own: the reference's CPU training path
-                (fp32, reconstruction backward, AdamW) restated in
-                oracle/model_ref.py, on a bounded sample of configs[3].
+  cpu_baseline  the reference's CPU path for the same step -- eager fp32
+                torch (nn.RMSNorm and F.silu(g) * v, forward and autograd
+                backward) -- on every CPU of the host this process may use,
+                with lscpu's description of the host; ``cpu_baseline_oracle``
+                is the C oracle (oracle/kernels_ref.c, OpenMP) on the same
+                step.  The train step carries its own: the reference's CPU
+                training path (fp32, reconstruction backward, AdamW) restated
+                in oracle/model_ref.py, on a bounded sample of configs[3].
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -284,6 +295,77 @@ def copy_ceilings(dev, launches: int) -> dict:
             run(i)
         out[name] = graph_time_ms(run, launches)
         del sets
+    torch.cuda.empty_cache()
+    return out
+
+
+STREAM_SHAPES = {  # kernel: (arrays read, arrays written, bytes per array)
+    "rms_fwd": (1, 1, ROWS * D_MODEL * 4),
+    "rms_bwd": (2, 1, ROWS * D_MODEL * 4),
+    "sw_fwd": (2, 1, ROWS * D_FF * 2),
+    "sw_bwd": (3, 2, ROWS * D_FF * 2),
+    # configs[0] forward + backward in one kernel: x, dy read... as one stream
+    "c1_one_kernel": (3, 2, ROWS * D_MODEL * 4),
+}
+
+
+def stream_floors(dev, launches: int) -> dict:
+    """The streaming floor of each kernel's read/write shape at its exact
+    byte count: rv_stream_floor (a hand-written kernel that only moves the
+    bytes: NR arrays read, NW written, 16 bytes per access, every load issued
+    before the first wait) swept over 1/2/4/8 vectors per thread and the four
+    load/store cache-hint combinations, each timed like the kernels
+    (graph_time_ms over rotating buffers, > 1.5 GB per shape), fastest kept.
+    ``rms_bwd_two_launch`` adds an empty 4-workgroup launch after each
+    2-read-1-write stream: the floor of any backward that finishes dweight in
+    a second launch.  ``c1_one_kernel`` moves configs[0]'s forward and
+    backward arrays (3 reads, 2 writes) in one kernel."""
+    import ctypes
+    import torch
+    from reversability_amd import _hip
+    lib = _hip.library()
+    out = {}
+    for name, (nr, nw, nbytes) in STREAM_SHAPES.items():
+        nsets = max(3, int(1.6e9 // ((nr + nw) * nbytes)))
+        sets, ptrs = [], []
+        for _ in range(nsets):
+            arrays = [torch.ones(nbytes // 4, device=dev) for _ in range(nr + nw)]
+            ins = (ctypes.c_void_p * 3)(*[a.data_ptr() for a in arrays[:nr]])
+            outs = (ctypes.c_void_p * 2)(*[a.data_ptr() for a in arrays[nr:]])
+            sets.append(arrays)
+            ptrs.append((ctypes.cast(ins, ctypes.c_void_p), ctypes.cast(outs, ctypes.c_void_p),
+                         ins, outs))
+        best = None
+        for vec in (1, 2, 4, 8):
+            for hints in range(4):
+                def run(i, stream=None, vec=vec, hints=hints):
+                    p = ptrs[i % len(ptrs)]
+                    rc = lib.rv_stream_floor(p[0], nr, p[1], nw, nbytes, vec, hints, stream)
+                    if rc:
+                        raise RuntimeError(f"rv_stream_floor failed with status {rc}")
+                for i in range(5):
+                    run(i)
+                ms = graph_time_ms(run, launches)
+                if best is None or ms < best[0]:
+                    best = (ms, vec, hints, run)
+        ms, vec, hints, run = best
+        moved = (nr + nw) * nbytes
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": moved,
+                     "GBps": round(moved / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_peak": round(moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "vec": vec, "nt_loads": bool(hints & 1), "nt_stores": bool(hints & 2)}
+        if name == "rms_bwd":
+            def two(i, stream=None, run=run):
+                run(i, stream)
+                rc = lib.rv_empty_kernel(4, stream)
+                if rc:
+                    raise RuntimeError(f"rv_empty_kernel failed with status {rc}")
+            ms2 = graph_time_ms(two, launches)
+            out["rms_bwd_two_launch"] = {
+                "us": round(ms2 * 1e3, 2), "bytes": moved,
+                "GBps": round(moved / (ms2 * 1e-3) / 1e9, 1),
+                "frac_of_peak": round(moved / (ms2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del sets, ptrs
     torch.cuda.empty_cache()
     return out
 
@@ -546,10 +628,46 @@ def mlp_block_bench(dev, steps: int = 20):
 
     us = _event_time_us(step, steps)
     flops = 70_061_654_016
+    moved = mlp_block_bytes()
     return {"workload": "configs[2] tiled MLP block 29x512 d256 f1024 tile 8192, fp16 autocast",
             "ms_per_step": round(us / 1e3, 4), "gemm_TFLOPs": round(flops / us / 1e6, 1),
             "frac_of_mfma_peak": round(flops / us / 1e6 / MFMA_PEAK_TFLOPS, 4),
-            "algorithmic_flop": flops}
+            "algorithmic_flop": flops, "algorithmic_bytes": moved,
+            "GBps": round(moved / us / 1e3, 1),
+            "frac_of_hbm_peak": round(moved / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def mlp_block_bytes(rows: int = 29 * 512, d: int = 256, f: int = 1024) -> int:
+    """Algorithmic HBM bytes of configs[2]'s block forward + backward: each
+    tensor of the dataflow read or written once at its stored precision (the
+    per-GEMM accounting of the up projection's arithmetic intensity, 224
+    FLOP/B: fp16 operands and fp16 outputs), the tiles' SwiGLU input u kept
+    from the forward for the backward (no recompute), the weights' fp16 casts
+    once per call:
+
+      weight casts    W_up, W_down fp32 r, fp16 w
+      RMSNorm fwd     x fp32 r, w r, y fp16 w, rstd w
+      up + SwiGLU     y r, W_up16 r, u = [gate | value] fp16 w, o fp16 w
+      down            o r, W_down16 r, out fp16 w
+      grad cast       dout fp32 r, fp16 w
+      dgate + SwiGLU' dout16 r, W_down16 r, u r, du fp16 w
+      dx              du r, W_up16 r, dy fp32 w
+      dW_down         dout16 r, o r, dW_down fp32 w
+      dW_up           du r, y r, dW_up fp32 w
+      RMSNorm bwd     x r, dy r, rstd r, w r, dx fp32 w, dw w"""
+    h, s = 2, 4  # fp16, fp32 bytes
+    wup, wdown = 2 * f * d, d * f
+    total = (wup + wdown) * (s + h)                               # weight casts
+    total += rows * d * s + d * s + rows * d * h + rows * s       # RMSNorm fwd
+    total += rows * d * h + wup * h + rows * 2 * f * h + rows * f * h  # up + SwiGLU
+    total += rows * f * h + wdown * h + rows * d * h              # down
+    total += rows * d * (s + h)                                   # grad cast
+    total += rows * d * h + wdown * h + 2 * rows * 2 * f * h      # dgate + SwiGLU bwd
+    total += rows * 2 * f * h + wup * h + rows * d * s            # dx
+    total += rows * d * h + rows * f * h + wdown * s              # dW_down
+    total += rows * 2 * f * h + rows * d * h + wup * s            # dW_up
+    total += 3 * rows * d * s + rows * s + 2 * d * s              # RMSNorm bwd
+    return total
 
 
 ATTN_SHAPES = {  # (batch, seq, heads, head_dim) of the attention inside configs[3] / [4]
@@ -645,6 +763,76 @@ def embedding_bench(dev, reps: int = 20):
             "bwd_us": round(bwd_us, 1), "bwd_GBps_upper": round(16 * d * n / bwd_us / 1e3, 1)}
 
 
+def host_cpu() -> dict:
+    """The host's CPU as lscpu reports it (model, sockets, cores per socket,
+    threads per core, logical CPUs) and the CPUs this process may run on."""
+    import subprocess
+    info = {"affinity_cpus": len(os.sched_getaffinity(0))}
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "CPU(s)": "logical_cpus"}
+    try:
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        text = ""
+    for line in text.splitlines():
+        key, _, value = line.partition(":")
+        if key.strip() in keys:
+            value = value.strip()
+            info[keys[key.strip()]] = int(value) if value.isdigit() else value
+    return info
+
+
+def cpu_baseline_torch(seconds: float, reps_min: int = 5):
+    """The reference's CPU path for configs[0] + configs[1], timed on this
+    host: eager torch in fp32 -- nn.RMSNorm (eps from finfo, the module
+    src/reversibility/model.py:62,64,79 builds) forward and its autograd
+    backward (dx, dweight), then F.silu(gate) * value (model.py:55-56) forward
+    and backward.  The reference's fused ops refuse CPU tensors
+    (kernels_v3.py:54-55, kernels.py:116-117) and its CPU path runs without
+    autocast (optimized.py:64-67), so configs[1] is fp32 here.  Threads: every
+    CPU this process may use (torch.set_num_threads).  Median of the timed
+    repetitions after two warm-ups, repeated for about ``seconds`` (at least
+    ``reps_min``); the value is the step's algorithmic bytes (STEP_BYTES, the
+    GPU step's unit of work) per second."""
+    import statistics
+    import torch
+    threads = len(os.sched_getaffinity(0))
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(1337)
+    norm = torch.nn.RMSNorm(D_MODEL)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.02 * torch.randn(D_MODEL, generator=g))
+    x = torch.randn(ROWS, D_MODEL, generator=g).requires_grad_(True)
+    gy = torch.randn(ROWS, D_MODEL, generator=g)
+    gate = torch.randn(ROWS, D_FF, generator=g).requires_grad_(True)
+    value = torch.randn(ROWS, D_FF, generator=g).requires_grad_(True)
+    sdy = torch.randn(ROWS, D_FF, generator=g)
+
+    def one():
+        y = norm(x)
+        torch.autograd.grad(y, (x, norm.weight), gy)
+        o = torch.nn.functional.silu(gate) * value
+        torch.autograd.grad(o, (gate, value), sdy)
+
+    for _ in range(2):
+        one()
+    times, t_start = [], time.perf_counter()
+    while len(times) < reps_min or time.perf_counter() - t_start < seconds:
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    torch.set_num_threads(saved)
+    per = statistics.median(times)
+    return {"value": round(STEP_BYTES / per / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "ms_per_step": round(per * 1e3, 3), "host": host_cpu(),
+            "sample": f"median of {len(times)} full steps (RMSNorm [14848,256] fwd+bwd + "
+                      f"SwiGLU [14848,1024] fwd+bwd) in eager fp32 torch on the CPU -- the "
+                      f"reference's CPU path -- after 2 warm-ups, "
+                      f"torch.set_num_threads({threads}); GB/s = the GPU step's algorithmic "
+                      f"bytes per second"}
+
+
 def cpu_baseline(seconds: float):
     """Oracle (C, OpenMP) on this host's cores: the same RMSNorm+SwiGLU step."""
     import numpy as np
@@ -733,13 +921,29 @@ def cpu_train_baseline(seconds: float, batch: int = 2):
 
 
 def load_traffic():
+    """HBM bytes per launch of the roofline kernel from profiles/traffic.json
+    (rocprofv3 FETCH_SIZE / WRITE_SIZE runs), and where they were measured:
+    the commit and the sha256 of the kernel's sources then.  A recorded
+    figure whose sources differ from the ones built now is stale: None."""
+    import hashlib
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
-        return None
+        return None, None
     try:
-        return json.loads(path.read_text()).get("swiglu_bwd_bytes_per_launch")
+        data = json.loads(path.read_text())
     except (OSError, ValueError):
-        return None
+        return None, None
+    where = data.get("measured_on") or {}
+    for name, digest in (where.get("sources_sha256") or {}).items():
+        try:
+            current = hashlib.sha256((ROOT / name).read_bytes()).hexdigest()
+        except OSError:
+            current = None
+        if current != digest:
+            return None, {"stale": True, **where}
+    if not where:
+        return None, None
+    return data.get("swiglu_bwd_bytes_per_launch"), where
 
 
 def main() -> int:
@@ -781,7 +985,19 @@ def main() -> int:
                    "frac_of_copy_ceiling": round(ceiling[n] / per_kernel[n], 4)}
                for n in per_kernel}
     ceiling_gbs = STEP_BYTES / (sum(ceiling.values()) * 1e-3) / 1e9
+    floors = stream_floors(dev, args.steps)
+    for n in per_kernel:
+        kernels[n]["stream_floor_us"] = floors[n]["us"]
+        kernels[n]["frac_of_stream_floor"] = round(floors[n]["us"] / kernels[n]["avg_us"], 4)
+    floor_step_us = sum(floors[n]["us"] for n in per_kernel)
+    floors["step"] = {"us": round(floor_step_us, 2),
+                      "GBps": round(STEP_BYTES / (floor_step_us * 1e-6) / 1e9, 1),
+                      "frac_of_peak": round(STEP_BYTES / (floor_step_us * 1e-6) / 1e9
+                                            / HBM_PEAK_GBS, 4),
+                      "value_over_floor": round(value / (STEP_BYTES / (floor_step_us * 1e-6)
+                                                         / 1e9), 4)}
     achieved = kernels["sw_bwd"]["GBps"]
+    traffic, traffic_where = load_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -810,9 +1026,11 @@ def main() -> int:
                          "what": "the step's bytes moved by torch's elementwise mul/add "
                                  "kernels of the same read/write shape, summed over the "
                                  "four kernels (copy_ceiling_us per kernel)"},
+        "stream_floor": floors,
         "roofline": {"bound": "hbm", "kernel": "swiglu_once<__half, true, 1> (SwiGLU bwd)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_measured_on": traffic_where,
                      "algorithmic_bytes": SW_BWD_BYTES},
         "kernels": kernels,
     }
@@ -826,7 +1044,8 @@ def main() -> int:
         if args.cpu_seconds > 0:
             line["train_step"]["cpu_baseline"] = cpu_train_baseline(args.cpu_seconds)
     if args.cpu_seconds > 0:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline_torch(args.cpu_seconds)
+        line["cpu_baseline_oracle"] = cpu_baseline(args.cpu_seconds / 2)
     print(json.dumps(line), flush=True)
     return 0
 

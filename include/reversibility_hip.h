@@ -485,6 +485,24 @@ int rv_embed_bwd(const int64_t* ids, int64_t batch, int64_t seq, const float* do
                  int tok_accumulate, float* dpos, int pos_accumulate,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement only (no counterpart in the reference; no hot-path result
+ * depends on them): the streaming floor a bandwidth-bound kernel is judged
+ * against.
+ */
+
+/* Read nin (1..3) arrays and write nout (1..2) arrays of `bytes` bytes each
+ * (a multiple of 16; 16-byte aligned device pointers; `in` and `out` are host
+ * arrays of device pointers), 16 bytes per access, `vec` (1, 2, 4 or 8)
+ * vectors per array and thread, every load issued before the first wait;
+ * hints bit 0 = non-temporal loads, bit 1 = non-temporal stores.  Each output
+ * is the xor of the inputs (output k with k xored into its first word). */
+int rv_stream_floor(const void* const* in, int nin, void* const* out, int nout, int64_t bytes,
+                    int vec, int hints, void* stream);
+
+/* An empty kernel of `blocks` workgroups: the cost of one more launch. */
+int rv_empty_kernel(int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,6 +92,8 @@ SIGNATURES = {
     "rv_embed_fwd": (_I, [_P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _P]),
     "rv_embed_bwd_workspace_bytes": (_I64, [_I64, _I64, _I64]),
     "rv_embed_bwd": (_I, [_P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I, _P, _I, _P, _I64, _P]),
+    "rv_stream_floor": (_I, [_P, _I, _P, _I, _I64, _I, _I, _P]),
+    "rv_empty_kernel": (_I, [_I, _P]),
 }
 ABI_VERSION = 3
 

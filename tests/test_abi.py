@@ -62,6 +62,14 @@ def test_argument_validation_without_device():
     assert lib.rv_midpoint_update(fake, fake, fake, fake, 1.0, 1, 16, _hip.RV_F16, _hip.RV_F32, None) == 3
     assert lib.rv_residual_axpy(fake, fake, fake, 1, -1, 0, 1, None) == 2
     assert lib.rv_add_rmsnorm_fwd(fake, fake, _hip.RV_F64, fake, fake, fake, fake, 4, 256, 1e-7, None) == 3
+    ptrs = (ctypes.c_void_p * 3)(4096, 4096, 4096)
+    arr = ctypes.cast(ptrs, ctypes.c_void_p)
+    assert lib.rv_stream_floor(None, 1, arr, 1, 64, 1, 0, None) == 1
+    assert lib.rv_stream_floor(arr, 4, arr, 1, 64, 1, 0, None) == 2  # at most 3 inputs
+    assert lib.rv_stream_floor(arr, 1, arr, 3, 64, 1, 0, None) == 2  # at most 2 outputs
+    assert lib.rv_stream_floor(arr, 1, arr, 1, 24, 1, 0, None) == 2  # whole 16-byte vectors
+    assert lib.rv_stream_floor(arr, 1, arr, 1, 64, 1, 4, None) == 3  # hint bits 0..1
+    assert lib.rv_empty_kernel(0, None) == 2
 
 
 @pytest.mark.parametrize("rows,width", [(1, 8), (14848, 256), (32768, 1024), (69, 33),
