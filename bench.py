@@ -1,11 +1,11 @@
 """Benchmark of the reversible-training hot path on one MI355X.
 
 Headline (``value``): fused RMSNorm + SwiGLU forward+backward throughput in
-algorithmic HBM GB/s.  One step = RMSNorm fwd + bwd over configs[0]
-(x fp32 [14848, 256]) followed by SwiGLU fwd + bwd over configs[1]
-(gate/up fp16 [14848, 1024]), launched through the C ABI; the timed steps
-are captured in one HIP graph and replayed (the eagerly launched step is
-reported beside it).  Algorithmic bytes per step (each tensor read or written
+algorithmic HBM GB/s.  One step = RMSNorm fwd over configs[0] (x fp32
+[14848, 256]), SwiGLU fwd + bwd over configs[1] (gate/up fp16 [14848, 1024]),
+RMSNorm bwd over configs[0] -- the order the ops run in a training step's MLP
+block -- launched through the C ABI; the timed steps are captured in one HIP
+graph and replayed (the eagerly launched step is reported beside it).  Algorithmic bytes per step (each tensor read or written
 once):
 
     RMSNorm fwd  x r, w r, y w, rstd w             30,469,120 B
@@ -164,7 +164,9 @@ class KernelStep:
             self.sw_sets.append(s)
         self.fns = {"rms_fwd": self.lib.rv_rmsnorm_fwd, "rms_bwd": self.lib.rv_rmsnorm_bwd,
                     "sw_fwd": self.lib.rv_swiglu_fwd, "sw_bwd": self.lib.rv_swiglu_bwd}
-        self.order = ["rms_fwd", "rms_bwd", "sw_fwd", "sw_bwd"]
+        # the order the ops run in a training step's MLP block: RMSNorm forward,
+        # SwiGLU forward, then the backward in reverse order
+        self.order = ["rms_fwd", "sw_fwd", "sw_bwd", "rms_bwd"]
         self.stream = torch.cuda.current_stream(dev).cuda_stream
 
     def set_for(self, name: str, i: int) -> dict:

@@ -94,9 +94,11 @@ int rv_rmsnorm_bwd(const float* x, const float* w, const float* dy,
  * (256 x 4096 fp32) that each GPU holds from the first call on that device
  * until the process ends.  The call allocates nothing (no hipMalloc / hipFree,
  * no library allocation); its first call on a device looks up the array's
- * address there.  width <= 4096 (RV_ERR_UNSUPPORTED above); the partial rows
+ * address there (hipGetSymbolAddress, no stream work: that first call may be
+ * made under graph capture).  width <= 4096 (RV_ERR_UNSUPPORTED above); the partial rows
  * (rv_rmsnorm_bwd_workspace_bytes) must fit the 4 MiB array -- for width <=
- * 256 one partial row per 64 .. 128 rows, so rows <= 524288 at width 256;
+ * 256 one partial row per ceil(rows / 256) rows (16 .. 128), so rows <=
+ * 524288 at width 256;
  * above 256 any rows (256 partial rows) -- (RV_ERR_WORKSPACE otherwise); and
  * the stream (if not null) must belong to the current device
  * (RV_ERR_UNSUPPORTED otherwise).  All calls on one GPU

@@ -43,8 +43,9 @@ using rv::wave_sum;
 //   forward, wider rows    8 blocks of 4 waves per CU, persistent, one row per
 //                          wave in flight
 //   backward, width <= 256 the same layout, blocks of 4 waves x 4 .. 8 four-row
-//                          groups (C1: 232 blocks of 64 rows), every row of a
-//                          block in flight at once (13.1 -> 11.9 us)
+//                          groups, the rows spread evenly over 256 blocks (C1:
+//                          256 blocks of 58 rows), every row of a block in
+//                          flight at once (13.1 -> 11.9 us; even spread 11.85)
 //   backward, wider rows   256 blocks of 4 .. 16 waves, ~128 rows per block
 // Stores of y / dx are streaming.
 #ifndef RV_RMS_FWD_BLOCKS_PER_CU
@@ -56,6 +57,7 @@ using rv::wave_sum;
 #ifndef RV_RMS_BWD_BLOCKS
 #define RV_RMS_BWD_BLOCKS 256
 #endif
+
 
 
 constexpr int kFwdWaves = 4;                 // waves per block, forward
@@ -548,8 +550,10 @@ constexpr int kGrpMaxLoads = 8;  // the fewest that keep the grid at <= 256 bloc
 // Loads of group k of the block: rows base + (k * kGrpWaves + wave) * 4 + lane/16,
 // clamped to end - 1; addresses are block-uniform base pointers plus 32-bit
 // lane offsets (a block's 16 NG rows).  The backward is the last reader of the
-// fp32 rows: streaming loads (C1: 12.3 -> 11.95 us; the forward keeps plain
-// loads, whose lines the backward of the same batch may still find cached).
+// fp32 rows and of an fp32 dy: streaming loads (x: C1 12.3 -> 11.95 us, dy as
+// well: 11.77 -> 11.51 us; the forward keeps plain loads, whose lines the
+// backward of the same batch may still find cached).  dx stores are streaming
+// too (plain stores: 11.77 -> 14.07 us).
 template <int VEC, int NG, bool FULL, typename G, bool ACC, bool PASS>
 __device__ __forceinline__ void grp_load(GrpTile<VEC, ACC, PASS> (&t)[NG],
                                          const float* __restrict__ x, const G* __restrict__ dy,
@@ -572,7 +576,8 @@ __device__ __forceinline__ void grp_load(GrpTile<VEC, ACC, PASS> (&t)[NG],
       const int col = lane_col<16>(v, lane);
       const unsigned off = (unsigned)(rc * width + (FULL || col < width ? col : width - 4));
       t[k].x[v] = rv::ld_f4s(xb + off);
-      t[k].g[v] = rv::load4f(gb + off);
+      if constexpr (std::is_same<G, float>::value) t[k].g[v] = rv::ld_f4s(gb + off);
+      else t[k].g[v] = rv::load4f(gb + off);
       if constexpr (ACC) t[k].h[v] = rv::ld_f4s(hb + off);
       if constexpr (PASS) t[k].p[v] = rv::ld_f4s(pb + off);
     }
@@ -584,16 +589,17 @@ __global__ __launch_bounds__(kGrpWaves * 64)
 void rms_bwd_grp(const float* __restrict__ x, const float* __restrict__ w,
                  const G* __restrict__ dy, const float* __restrict__ rstd,
                  float* __restrict__ dx, float* __restrict__ partial,
-                 int64_t rows, int width,
+                 int64_t rows, int width, int rows_per_block,
                  const float* __restrict__ dh = nullptr, __half* __restrict__ dx16 = nullptr,
                  const float* __restrict__ dpass = nullptr) {
   constexpr int GL = 16;  // lanes per row
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane >> 4;
-  constexpr int kRows = kGrpWaves * NG * 4;  // rows per block
-  const int64_t start = (int64_t)blockIdx.x * kRows;
-  const int64_t end = start + kRows < rows ? start + kRows : rows;
+  // rows_per_block <= kGrpWaves * NG * 4 (the plan picks NG so); slots past
+  // the block's rows load a valid row and are masked out
+  const int64_t start = (int64_t)blockIdx.x * rows_per_block;
+  const int64_t end = start + rows_per_block < rows ? start + rows_per_block : rows;
   const float fwidth = (float)width;
 
   // The weight is staged once per block through LDS: wave 0 loads it ahead of
@@ -630,7 +636,7 @@ void rms_bwd_grp(const float* __restrict__ x, const float* __restrict__ w,
     acc[v] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   {
-    const int nrows = (int)(end - start);  // 1 .. kRows
+    const int nrows = (int)(end - start);  // 1 .. rows_per_block
     float* dxb = dx + start * width;
     __half* d16b = H16 ? dx16 + start * width : nullptr;
 #pragma unroll
@@ -775,40 +781,44 @@ void rms_bwd_scalar(const float* __restrict__ x, const float* __restrict__ w,
 }
 
 // dw[col] = sum over parts of partial[part][col] (row-major, one contiguous
-// row per backward block).  A block covers 64 columns (lane = column) with
-// kRedWaves waves; wave k sums parts k, k + kRedWaves, ... in order, in
-// batches of kRedPerWave parts whose loads are all issued before the batch's
-// first add (one memory round trip per batch), then the waves' sums are
-// added in wave order through LDS.  Fixed order throughout.
-constexpr int kRedWaves = 16;
-constexpr int kRedPerWave = 16;
+// row per backward block).  A block covers kRedCols columns with kRedGroups
+// groups of kRedCols threads (thread = group * kRedCols + column): group g
+// sums parts g, g + kRedGroups, ... in order, in batches of kRedPerGroup parts
+// whose loads are all issued before the batch's first add (one memory round
+// trip per batch), then the groups' sums are added in group order through
+// LDS.  Fixed order throughout.  Narrow blocks spread the partial rows' reads
+// over many compute units: at width 256, 32 blocks of 8 KB each (C1 backward
+// with its reduce 11.51 -> 11.20 us against 4 blocks of 64 columns, one CU
+// pulling 64 KB; 16 or 32 columns per block 11.29).
+constexpr int kRedGroups = 16;
+constexpr int kRedCols = 8;
+constexpr int kRedPerGroup = 16;
 
-__global__ __launch_bounds__(kRedWaves * 64)
+__global__ __launch_bounds__(kRedGroups * kRedCols)
 void rms_dw_reduce(const float* __restrict__ partial, float* __restrict__ dw,
                    int width, int nparts) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + lane;
+  const int g = threadIdx.x / kRedCols, cl = threadIdx.x % kRedCols;
+  const int col = blockIdx.x * kRedCols + cl;
   const int col_c = col < width ? col : width - 1;
   float s = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += kRedWaves * kRedPerWave) {
-    float v[kRedPerWave];
+  for (int p0 = 0; p0 < nparts; p0 += kRedGroups * kRedPerGroup) {
+    float v[kRedPerGroup];
 #pragma unroll
-    for (int i = 0; i < kRedPerWave; ++i) {
-      const int part = p0 + wave + i * kRedWaves;
+    for (int i = 0; i < kRedPerGroup; ++i) {
+      const int part = p0 + g + i * kRedGroups;
       v[i] = partial[(int64_t)(part < nparts ? part : nparts - 1) * width + col_c];
     }
 #pragma unroll
-    for (int i = 0; i < kRedPerWave; ++i)
-      if (p0 + wave + i * kRedWaves < nparts) s = s + v[i];
+    for (int i = 0; i < kRedPerGroup; ++i)
+      if (p0 + g + i * kRedGroups < nparts) s = s + v[i];
   }
-  __shared__ float red[kRedWaves][64];
-  red[wave][lane] = s;
+  __shared__ float red[kRedGroups][kRedCols];
+  red[g][cl] = s;
   __syncthreads();
-  if (wave == 0) {
-    float t = red[0][lane];
+  if (threadIdx.x < kRedCols) {
+    float t = red[0][cl];
 #pragma unroll
-    for (int k = 1; k < kRedWaves; ++k) t = t + red[k][lane];
+    for (int k = 1; k < kRedGroups; ++k) t = t + red[k][cl];
     if (col < width) dw[col] = t;
   }
 }
@@ -823,11 +833,11 @@ struct BwdPlan {
 
 // Wide rows (width > 256): 256 blocks = one per compute unit on a 256-CU
 // MI355X, all resident at once, every block with the same number of rows (no
-// partial second wave of blocks).  Rows of width <= 256 (rms_bwd_grp): blocks
-// of 64 .. 128 rows, at most 256 blocks up to 32768 rows.  The counts depend
-// on rows and width only, not on
-// the device, so the dw summation order -- and therefore dw bit for bit --
-// does not depend on the device.  (Reducing the partials inside the backward
+// partial second wave of blocks).  Rows of width <= 256 (rms_bwd_grp): 256
+// blocks of ceil(rows / 256) rows (at least 16, at most 128: more blocks
+// beyond 32768 rows).  The counts depend on rows and width only, not on the
+// device, so the dw summation order -- and therefore dw bit for bit -- does
+// not depend on the device.  (Reducing the partials inside the backward
 // kernel instead -- the last block to finish sums them -- needs device-scope
 // release/acquire fences, which write back the per-XCD L2 on MI355X and
 // measured 4-15x slower than this second launch.)
@@ -837,18 +847,30 @@ constexpr int64_t kBwdTargetBlocks = RV_RMS_BWD_BLOCKS;
 // the vector path): the partial-row plan depends on it.
 constexpr bool bwd_narrow(int64_t width) { return width <= 256; }
 
-// Groups per wave of rms_bwd_grp for this many rows: 4, 5, 6 or 8 (the
-// instantiated counts).
-int grp_loads(int64_t rows) {
-  const int64_t per_wave = (rows + kBwdTargetBlocks * kGrpWaves * 4 - 1) /
-                           (kBwdTargetBlocks * kGrpWaves * 4);
+// Rows per block of rms_bwd_grp: the rows spread evenly over
+// kBwdTargetBlocks blocks (every compute unit of a 256-CU MI355X gets one
+// block), at least 16 and at most kGrpWaves * 4 * kGrpMaxLoads = 128 rows per
+// block (more blocks beyond 32768 rows).  C1: 14848 rows -> 256 blocks of 58
+// rows (232 blocks of 64 rows left 24 CUs idle: backward 11.99-12.04 ->
+// 11.85-11.86 us).
+int64_t grp_rows_per_block(int64_t rows) {
+  int64_t rpb = (rows + kBwdTargetBlocks - 1) / kBwdTargetBlocks;
+  if (rpb < 16) rpb = 16;
+  if (rpb > kGrpWaves * 4 * kGrpMaxLoads) rpb = kGrpWaves * 4 * kGrpMaxLoads;
+  return rpb;
+}
+
+// Four-row groups per wave of rms_bwd_grp holding a block of rpb rows: 4, 5,
+// 6 or 8 (the instantiated counts), the fewest with kGrpWaves * 4 * NG >= rpb.
+int grp_loads(int64_t rpb) {
+  const int64_t per_wave = (rpb + kGrpWaves * 4 - 1) / (kGrpWaves * 4);
   if (per_wave <= kGrpMinLoads) return kGrpMinLoads;
   if (per_wave <= 6) return (int)per_wave;
   return kGrpMaxLoads;
 }
 
 BwdPlan plan_bwd(int64_t rows, int64_t width) {
-  int64_t rpb = bwd_narrow(width) ? (int64_t)kGrpWaves * 4 * grp_loads(rows)
+  int64_t rpb = bwd_narrow(width) ? grp_rows_per_block(rows)
                                   : (rows + kBwdTargetBlocks - 1) / kBwdTargetBlocks;
   if (rpb < 1) rpb = 1;
   BwdPlan p;
@@ -990,15 +1012,16 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
   if (dpass != nullptr && (dh != nullptr || dx16 == nullptr)) return RV_ERR_UNSUPPORTED;
   if (vec && bwd_narrow(iw)) {
     const dim3 gblock(kGrpWaves * 64);
-    const int ng = grp_loads(rows);
+    const int ng = grp_loads(p.rows_per_block);
+    const int rpb = (int)p.rows_per_block;
 #define RV_BWD_GRP_K(V, NG, ACC, H16, PASS)                                                       \
   do {                                                                                            \
     if (iw == 64 * (V))                                                                           \
       hipLaunchKernelGGL((rms_bwd_grp<V, NG, true, G, ACC, H16, PASS>), grid, gblock, 0, s, x, w, \
-                         dy, rstd, dx, partial, rows, iw, dh, dx16, dpass);                       \
+                         dy, rstd, dx, partial, rows, iw, rpb, dh, dx16, dpass);                  \
     else                                                                                          \
       hipLaunchKernelGGL((rms_bwd_grp<V, NG, false, G, ACC, H16, PASS>), grid, gblock, 0, s, x,   \
-                         w, dy, rstd, dx, partial, rows, iw, dh, dx16, dpass);                    \
+                         w, dy, rstd, dx, partial, rows, iw, rpb, dh, dx16, dpass);               \
   } while (0)
 #define RV_BWD_GRP_NG(V, NG)                                                      \
   do {                                                                            \
@@ -1063,8 +1086,8 @@ int launch_bwd(const float* x, const float* w, const G* dy, const float* rstd, f
   }
   int st = rv_host::check_launch();
   if (st != RV_OK) return st;
-  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + 63) / 64)),
-                     dim3(kRedWaves * 64), 0, s, partial, dw, iw, p.nparts);
+  hipLaunchKernelGGL(rms_dw_reduce, dim3((unsigned)((iw + kRedCols - 1) / kRedCols)),
+                     dim3(kRedGroups * kRedCols), 0, s, partial, dw, iw, p.nparts);
   return rv_host::check_launch();
 }
 

@@ -76,15 +76,12 @@ def test_argument_validation_without_device():
                                         (16896, 256), (24000, 256), (27000, 256),
                                         (40000, 256), (300, 260)])
 def test_workspace_size_is_device_independent(rows, width):
-    """Partial rows: width <= 256 -- one per 16 g rows, g = ceil(rows / 4096)
-    groups per wave clamped to 4 .. 8 (7 taken as 8); wider -- 256 blocks of
-    ceil(rows / 256) rows."""
+    """Partial rows: one per block of ceil(rows / 256) rows -- for width <= 256
+    at least 16 and at most 128 rows per block."""
     n = _hip.rmsnorm_workspace_bytes(rows, width)
+    per_block = -(-rows // 256)
     if width <= 256:
-        g = min(max(-(-rows // 4096), 4), 8)
-        per_block = 16 * (8 if g == 7 else g)
-    else:
-        per_block = -(-rows // 256)
+        per_block = min(max(per_block, 16), 128)
     parts = -(-rows // per_block)
     assert n == parts * width * 4
 

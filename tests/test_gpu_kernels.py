@@ -546,11 +546,16 @@ def test_fused_norm_paths_with_unaligned_weight_take_the_unfused_path(cuda_devic
 
 @pytest.mark.parametrize("rows,width", [(1, 256), (15, 256), (17, 100), (255, 1020),
                                         (257, 1024), (14848, 256), (32768, 1024), (4097, 1028),
-                                        (33, 66)])
+                                        (33, 66), (16896, 256), (20000, 256), (24000, 256),
+                                        (30000, 256), (40000, 256), (40001, 132),
+                                        (70000, 256)])
 def test_rmsnorm_bwd_reduction_repeats(cuda_device, rows, width):
     """The backward's fixed-order dweight reduction over its partial rows (one
-    to 256 of them, vector and scalar paths): dx and dw match the oracle, and
-    fifty calls on one workspace give the same bits."""
+    to 547 of them -- beyond 256 the reduce sums them in several batches --
+    vector and scalar paths, and at width <= 256 every instantiated group
+    count: 4, 5 (16896, 20000 rows), 6 (24000), 8 (30000 and above, 128 rows
+    per block)): dx and dw match the oracle, and fifty calls on one workspace
+    give the same bits."""
     lib = _hip.library()
     g = torch.Generator().manual_seed(rows * 7 + width)
     x = torch.randn(rows, width, generator=g)
