@@ -187,6 +187,38 @@ def test_every_tile_shape_gives_identical_bits(cuda_device, rows, d, f):
     assert lib.rv_gemm_force_shape(lib.rv_gemm_num_shapes()) != 0
 
 
+def test_dgate_every_shape_repeats(cuda_device):
+    """dgate + SwiGLU backward at 8192 x 256 x 1024 (the configuration an
+    epilogue variant addressing u through buffer resources once failed in,
+    for the tile shapes whose waves own 64 columns) on every tile shape, five
+    calls each: identical bits across shapes and calls, and the oracle's bar
+    on the kernel's own d_o."""
+    from reversability_amd._hip import library
+    lib = library()
+    rows, d, f = 8192, 256, 1024
+    _, down = weights(d, f, cuda_device)
+    g = torch.Generator().manual_seed(3)
+    dy = torch.randn(rows, d, generator=g).half().to(cuda_device)
+    u = torch.randn(rows, 2 * f, generator=g).half().to(cuda_device)
+    down16 = mlp.cast_f16(down)
+    first = None
+    try:
+        for shape in range(lib.rv_gemm_num_shapes()):
+            assert lib.rv_gemm_force_shape(shape) == 0
+            for call in range(5):
+                du = mlp.dgate(dy, down16, u)
+                torch.cuda.synchronize()
+                if first is None:
+                    first = du.clone()
+                assert torch.equal(du, first), (shape, call)
+    finally:
+        assert lib.rv_gemm_force_shape(-1) == 0
+    d_o = (dy.float() @ down16.float()).half()
+    du_ref = torch.from_numpy(oracle.swiglu_bwd(u.cpu().numpy(), d_o.cpu().numpy()))
+    assert rel_l2(first.cpu(), du_ref) < 2e-3
+    assert float((ulps(first, du_ref) > 2).float().mean()) < 0.01
+
+
 def test_multi_tensor_cast_and_prefetch(cuda_device):
     """rv_cast_f32_f16_multi equals rv_cast_f32_f16 per tensor, bit for bit
     (ragged sizes, more tensors than one launch takes); prefetch_casts fills
