@@ -581,3 +581,30 @@ def test_rmsnorm_bwd_reduction_repeats(cuda_device, rows, width):
     for got, ref in ((first[0], odx), (first[1], odw)):
         err = np.abs(got.cpu().numpy().astype(np.float64) - ref).max() / np.abs(ref).max()
         assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("nin,nout", [(1, 1), (2, 1), (3, 2)])
+@pytest.mark.parametrize("vec,hints", [(1, 0), (2, 3), (8, 1)])
+def test_stream_floor_kernel_moves_the_bytes(cuda_device, nin, nout, vec, hints):
+    """rv_stream_floor (measurement only): every output vector is the xor of the
+    inputs' vectors (output k with k xored into its first word), a ragged size
+    included, so the timed kernel really reads and writes every byte."""
+    import ctypes
+    lib = _hip.library()
+    n = 1000 * 4 + 4  # int32 words: 1001 vectors of 16 bytes, not a multiple of the block
+    g = torch.Generator().manual_seed(nin * 10 + nout)
+    ins = [torch.randint(-2 ** 31, 2 ** 31 - 1, (n,), generator=g, dtype=torch.int32).to(cuda_device)
+           for _ in range(nin)]
+    outs = [torch.zeros(n, dtype=torch.int32, device=cuda_device) for _ in range(nout)]
+    ip = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in ins])
+    op = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in outs])
+    assert lib.rv_stream_floor(ctypes.cast(ip, ctypes.c_void_p), nin, ctypes.cast(op, ctypes.c_void_p),
+                               nout, n * 4, vec, hints, _hip._stream(ins[0])) == 0
+    torch.cuda.synchronize()
+    ref = ins[0].clone()
+    for t in ins[1:]:
+        ref ^= t
+    for k, o in enumerate(outs):
+        expect = ref.clone().view(-1, 4)
+        expect[:, 0] ^= k
+        assert torch.equal(o.view(-1, 4), expect), k
