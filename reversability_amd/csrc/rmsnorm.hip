@@ -526,14 +526,15 @@ void rms_bwd_vec(const float* __restrict__ x, const float* __restrict__ w,
 // Backward, width % 4 == 0 and width <= 256: the forward's 16-lanes-per-row
 // layout (four rows per wave, lane l on row l/16 of its group, float4 number
 // v*16 + l%16 of the row).  Block b owns rows [b*R, min((b+1)*R, rows)),
-// R = 16 NG; its 4 NG four-row groups are dealt to the four waves
-// round-robin, and each wave issues the loads of its NG groups before
-// finishing any of them: every row of the block is in flight at once.  NG
-// (4 .. 8) is the fewest that keep the grid at one block per compute unit
-// (256 blocks; C1: 232 blocks of 64 rows), so no compute unit streams two
-// blocks' rows while others idle.  dweight per column: each lane sums its
-// own rows in order, then the block sums (wave, row-in-group) in order
-// through LDS and writes one contiguous partial row.
+// R = ceil(rows / 256) (16 .. 128): the rows spread evenly over 256 blocks,
+// one per compute unit (C1: 256 blocks of 58 rows), so no compute unit streams
+// two blocks' rows while others idle.  The block's 4 NG four-row slots (NG =
+// 4, 5, 6 or 8, the fewest with 16 NG >= R; slots past R are masked) are
+// dealt to the four waves round-robin, and each wave issues the loads of its
+// NG groups before finishing any of them: every row of the block is in
+// flight at once.  dweight per column: each lane sums its own rows in order,
+// then the block sums (wave, row-in-group) in order through LDS and writes
+// one contiguous partial row.
 // ---------------------------------------------------------------------------
 template <int VEC, bool ACC, bool PASS>
 struct GrpTile {
