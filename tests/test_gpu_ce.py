@@ -102,12 +102,14 @@ def test_rejects_cpu_and_bad_inputs(cuda_device):
         TiledCrossEntropy.apply(x.t(), torch.tensor([0, 1, 2], device=cuda_device))
 
 
-@pytest.mark.parametrize("rows,d,vocab", [(1000, 256, 50257), (333, 128, 1001), (64, 256, 64)])
+@pytest.mark.parametrize("rows,d,vocab", [(1000, 256, 50257), (333, 128, 1001), (64, 256, 64),
+                                           (64, 64, 70001)])
 def test_tied_head_ce_matches_autograd(cuda_device, rows, d, vocab):
-    """The padded-stride head + fused CE (forward and backward in one call)
-    against autograd of autocast F.linear + cross_entropy_sum on the same fp16
-    operands: the same loss and gradients up to the GEMMs' fp32 accumulation
-    order (the padded logits run other hipBLASLt kernels)."""
+    """The padded-stride head + fused CE (forward and backward in one call;
+    two passes above 65536 columns) against autograd of autocast F.linear +
+    cross_entropy_sum on the same fp16 operands: the same loss and gradients
+    up to the GEMMs' fp32 accumulation order (the padded logits run other
+    hipBLASLt kernels)."""
     from reversability_amd.kernels import padded_head, tied_head_ce
     g = torch.Generator().manual_seed(5)
     x16 = torch.randn(rows, d, generator=g).half().to(cuda_device)
@@ -122,7 +124,9 @@ def test_tied_head_ce_matches_autograd(cuda_device, rows, d, vocab):
     hr = w.half().requires_grad_(True)
     ref = cross_entropy_sum(torch.nn.functional.linear(xr, hr), labels)
     (ref * 0.37).backward()
-    assert abs(float(loss) - float(ref)) <= 1e-3 * abs(float(ref))
+    ref = float(ref.detach())
+    assert abs(float(loss) - ref) <= 1e-3 * abs(ref)
+    assert dx16.shape == (rows, d) and dw16.shape == (vocab, d) and dw16.is_contiguous()
     for got, want in ((dx16, xr.grad), (dw16, hr.grad)):
         assert got.dtype == torch.float16
         rel = float((got.float() - want.float()).norm() / want.float().norm())
