@@ -306,7 +306,7 @@ STREAM_SHAPES = {  # kernel: (arrays read, arrays written, bytes per array)
     "rms_bwd": (2, 1, ROWS * D_MODEL * 4),
     "sw_fwd": (2, 1, ROWS * D_FF * 2),
     "sw_bwd": (3, 2, ROWS * D_FF * 2),
-    # configs[0] forward + backward in one kernel: x, dy read... as one stream
+    # configs[0]'s forward and backward bytes in one launch: x (read by both), dy; y, dx
     "c1_one_kernel": (3, 2, ROWS * D_MODEL * 4),
 }
 
