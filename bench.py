@@ -424,8 +424,8 @@ assert step_flop(TRAIN_CONFIGS["c5"]["model"], 16) == 59_596_093_784_064
 
 # Cached-head token chunk: the reference probes 1024 on a 16 GB T4
 # (scripts/benchmark_midpoint_v3.py:174); on a 288 GB MI355X one chunk covers
-# the whole batch (C4 logits: 1.7 GB fp16), measured fastest (C4 14.7 ms vs
-# 19.4 ms at 1024).  None = the whole batch.
+# the whole batch (C4 logits: 1.7 GB fp16), measured fastest (C4 6.84 ms vs
+# 7.23 ms at 8448 tokens and 9.01 ms at 2048).  None = the whole batch.
 HEAD_CHUNK = None
 
 # TiledMLP token tile: the reference probes 8192 (scripts/benchmark_midpoint_v3.py),
