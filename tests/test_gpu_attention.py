@@ -149,7 +149,7 @@ def test_enable_attention_matches_reference_module(cuda_device):
             logits = m(ids)
             loss = F.cross_entropy(logits.flatten(0, 1).float(), ids.flatten())
         loss.backward()
-        losses.append(float(loss))
+        losses.append(float(loss.detach()))
         grads.append({n: p.grad.float() for n, p in m.named_parameters()})
     assert abs(losses[0] - losses[1]) <= 1e-3 * abs(losses[0])
     for n, g in grads[0].items():
