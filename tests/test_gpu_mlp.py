@@ -238,3 +238,34 @@ def test_multi_tensor_cast_and_prefetch(cuda_device):
     # outside a block it does nothing
     mlp.prefetch_casts(ws)
     assert mlp._weight_cache is None
+
+
+def test_first_call_under_graph_capture(cuda_device):
+    """An activation GEMM whose first call for its shape is made while the
+    stream is captured does not tune (tuning synchronises): it takes the rule's
+    tile shape, and its replays give the bits of the same call made eagerly
+    afterwards (which tunes and may pick another shape: every shape gives the
+    same bits).  Replays are checked with eager work and synchronisations
+    between them."""
+    rows, d, f = 3331, 256, 1024  # a row count no other test uses: a new tuning key
+    _, down = weights(d, f, cuda_device, seed=11)
+    down16 = mlp.cast_f16(down)
+    o = (0.5 * torch.randn(rows, f, generator=torch.Generator().manual_seed(12))).half()
+    o = o.to(cuda_device)
+    y_graph = torch.empty(rows, d, device=cuda_device, dtype=torch.float16)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
+        mlp.down(o, down16, y_graph)
+    torch.cuda.current_stream().wait_stream(stream)
+    y_eager = mlp.down(o, down16, torch.empty(rows, d, device=cuda_device, dtype=torch.float16))
+    torch.cuda.synchronize()
+    assert within_gemm_bound(y_eager, o, down16, f)
+    for _ in range(3):
+        y_graph.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_eager)
+        mlp.down(o, down16, torch.empty_like(y_eager))  # eager work between replays
