@@ -875,7 +875,10 @@ int run_act(GemmArgs a, int64_t n_cols, hipStream_t s) {
 // Weight-gradient plan for an ni x nj output reduced over `rows` tokens: tile
 // shape and split count minimising a simple cost (MFMA time at a per-shape
 // efficiency, divided by the fraction of the grid's CU rounds that hold a
-// workgroup, plus the partial sums' HBM round trip at ~500 flop per byte).
+// workgroup, plus the partial sums' HBM round trip at ~250 flop per byte; at
+// 500 the 8192-token tiles' weight gradients kept fewer splits on smaller
+// tiles and took 45.3 us (d 256, f 1024) and 267 us (d 1024, f 4096) against
+// 42.6 and 261 us).
 // The split count is the largest that keeps tiles x splits within one round
 // of the CUs: a grid a few workgroups past the CU count (C5's qkv weight
 // gradient: 96 tiles x 3 splits = 288) leaves those CUs a second turn and
@@ -909,7 +912,7 @@ WgradPlan plan_wgrad(int64_t rows, int64_t ni, int64_t nj) {
     const double fill = (double)wgs / (double)(rounds * kCUs);
     const double flops = 2.0 * rows * ni * nj / (eff[i] * fill);
     const double bytes = splits > 1 ? 8.0 * splits * ni * nj : 0.0;
-    const double cost = flops + 500.0 * bytes;
+    const double cost = flops + 250.0 * bytes;
     if (best.shape < 0 || cost < best_cost) {
       best = WgradPlan{i, ni / t.bm, nj / t.bn, splits, chunk};
       best_cost = cost;
