@@ -22,7 +22,7 @@ def fp16_ulp(t: torch.Tensor) -> torch.Tensor:
 
 
 def rel_l2(a, b):
-    a, b = a.double(), b.double().to(a.device)
+    a, b = a.detach().double(), b.detach().double().to(a.device)
     return float((a - b).norm() / b.norm().clamp_min(1e-30))
 
 
