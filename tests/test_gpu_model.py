@@ -240,7 +240,8 @@ def test_tiled_mlp_boundary_gate(cuda_device):
         inc = sum((p.detach() - u).double().square().sum().item()
                   for p, u in zip(left.parameters(), old))
         row = {"gradient_relative_l2": grad,
-               "loss_relative": float((loss - other).abs() / loss.abs().clamp_min(1e-12)),
+               "loss_relative": float((loss - other).detach().abs()
+                                      / loss.detach().abs().clamp_min(1e-12)),
                "optimizer_step_max_absolute": max(
                    float(((p.detach() - u) - (q.detach() - v)).abs().max())
                    for p, q, u, v in zip(left.parameters(), right.parameters(), old, old_r)),
