@@ -1063,7 +1063,7 @@ int rv_mlp_dgate(const void* dy, const void* w_down, const void* u, int64_t rows
   if (!dy || !w_down || !u || !du) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0) return RV_ERR_BAD_SIZE;
   if (d % kBK || f % 128) return RV_ERR_UNSUPPORTED;
-  if (!ok16(dy) || !ok16(w_down)) return RV_ERR_UNSUPPORTED;
+  if (!ok16(dy) || !ok16(w_down) || !ok16(u) || !ok16(du)) return RV_ERR_UNSUPPORTED;
   if (!fits32(rows * d) || !fits32(d * f)) return RV_ERR_UNSUPPORTED;
   GemmArgs a{};
   a.a = static_cast<const __half*>(dy); a.lda = d; a.a_bytes = rows * d * 2;
@@ -1079,7 +1079,7 @@ int rv_mlp_dx(const void* du, const void* w_up, int64_t rows, int64_t d, int64_t
   if (!du || !w_up || !dx) return RV_ERR_NULL_POINTER;
   if (rows <= 0 || d <= 0 || f <= 0) return RV_ERR_BAD_SIZE;
   if ((2 * f) % kBK || d % 128) return RV_ERR_UNSUPPORTED;
-  if (!ok16(du) || !ok16(w_up)) return RV_ERR_UNSUPPORTED;
+  if (!ok16(du) || !ok16(w_up) || !ok16(dx)) return RV_ERR_UNSUPPORTED;
   if (!fits32(rows * 2 * f) || !fits32(2 * f * d)) return RV_ERR_UNSUPPORTED;
   GemmArgs a{};
   a.a = static_cast<const __half*>(du); a.lda = 2 * f; a.a_bytes = rows * 2 * f * 2;

@@ -129,6 +129,44 @@ def test_rmsnorm_fp16_entry_points_validate_without_device():
     assert lib.rv_rmsnorm_bwd_f16(fake, fake, fake, fake, fake, fake, None, 0, 4, 256, None) == 4
 
 
+def test_gemm_entry_points_validate_without_device():
+    """The MFMA GEMM entry points refuse null pointers (1), bad sizes (2),
+    widths the tiles do not cover and any operand or output that is not
+    16-byte aligned (3), and a missing workspace (4), before any launch."""
+    lib = _hip.library()
+    fake = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4104)  # 8-byte, not 16-byte, aligned
+    rows, d, f = 64, 256, 1024
+    assert lib.rv_mlp_up_swiglu(None, d, fake, rows, d, f, fake, None, None) == 1
+    assert lib.rv_mlp_up_swiglu(fake, d, fake, 0, d, f, fake, None, None) == 2
+    assert lib.rv_mlp_up_swiglu(fake, d, fake, rows, 100, f, fake, None, None) == 3
+    assert lib.rv_mlp_up_swiglu(fake, d, fake, rows, d, f, odd, None, None) == 3
+    assert lib.rv_mlp_up_swiglu(fake, d, fake, rows, d, f, fake, odd, None) == 3
+    assert lib.rv_mlp_down(fake, fake, rows, d, f, odd, None) == 3
+    assert lib.rv_mlp_down(fake, fake, rows, 192, f, fake, None) == 3  # d % 128
+    for which in range(4):  # dy, w_down, u, du
+        ptrs = [fake] * 4
+        ptrs[which] = odd
+        assert lib.rv_mlp_dgate(ptrs[0], ptrs[1], ptrs[2], rows, d, f, ptrs[3], None) == 3
+    assert lib.rv_mlp_dgate(fake, fake, None, rows, d, f, fake, None) == 1
+    for which in range(3):  # du, w_up, dx
+        ptrs = [fake] * 3
+        ptrs[which] = odd
+        assert lib.rv_mlp_dx(ptrs[0], ptrs[1], rows, d, f, ptrs[2], None) == 3
+    need = lib.rv_mlp_wgrad_workspace_bytes(rows, d, f)
+    assert need >= 0
+    if need:
+        assert lib.rv_mlp_wgrad(fake, fake, fake, fake, d, rows, d, f, fake, fake, 0, None, 0,
+                                None) == 4
+    assert lib.rv_mlp_wgrad(fake, fake, fake, fake, d, rows, d, f, odd, fake, 0, fake, 1 << 30,
+                            None) == 3
+    assert lib.rv_linear_fwd(fake, 256, fake, rows, 256, 768, odd, None) == 3
+    assert lib.rv_linear_fwd(fake, 100, fake, rows, 256, 768, fake, None) == 2  # ldx < in
+    assert lib.rv_linear_dx(fake, fake, rows, 256, 768, fake, _hip.RV_F64, None) == 3
+    assert lib.rv_linear_dx(fake, fake, rows, 256, 768, odd, _hip.RV_F16, None) == 3
+    assert lib.rv_linear_dw(fake, fake, 256, rows, 256, 768, odd, 0, fake, 1 << 30, None) == 3
+
+
 def test_fused_cross_entropy_validates_without_device():
     lib = _hip.library()
     fake = ctypes.c_void_p(4096)
